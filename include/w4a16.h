@@ -1,0 +1,116 @@
+/*
+ * w4a16.h -- C ABI of the MI355X (gfx950) W4A16 GEMM library ``libw4a16_hip.so``.
+ *
+ *   y[M, N] = x[M, K] @ W^T,   W[n, k] = (q[n, k] - 8) * scales[k / G, n]
+ *
+ * x: fp16 [M, K] row-major.  scales: fp16 [K/G, N] row-major, G = K / (rows of scales) in {64, 128}.
+ * Wp: int32 [N*K/8] packed nibbles in the reference's layout [N/16][K/64][32][4]
+ * (reference tests/quant.py:34-48), read unchanged.  y: fp16 [M, N] row-major.
+ *
+ * Plain C types only (no torch, no HIP headers): device buffers are passed as pointers,
+ * the HIP stream as an opaque ``void*`` (a ``hipStream_t``).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   w4a16_plan_create      validation + routing + tile selection of
+ *                          w4a16_gemm_cuda (src/vectorized/kernel.cu:218-249),
+ *                          dispatch_prefill / pf_select (kernel.cu:142-156, 174-201)
+ *   w4a16_launch           the launches of dispatch<G> / try_launch (kernel.cu:19-53) and
+ *                          pf_launch / pf_launch_st (kernel.cu:117-138)
+ *   w4a16_query_device     the device-attribute queries and occupancy probe cache
+ *                          (kernel.cu:39-41, 72-115, 177-182)
+ *   w4a16_gemm (pybind11, src/vectorized/extension.cpp:5-9) is re-exposed by the torch
+ *   extension module ``w4a16_opt`` built on top of this ABI.
+ */
+#ifndef W4A16_H_
+#define W4A16_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A16_ABI_VERSION 1
+
+/* Status codes. */
+#define W4A16_OK            0
+#define W4A16_ERR_INVALID   1   /* argument / shape contract violated (message in err buffer) */
+#define W4A16_ERR_NO_CONFIG 2   /* no kernel configuration fits the device limits            */
+#define W4A16_ERR_HIP       3   /* a HIP runtime call failed                                   */
+#define W4A16_ERR_WORKSPACE 4   /* workspace / counter buffer missing or too small            */
+
+/* Variant ids (kernel.cu:217-224): -1 auto, 0 decode kernel, 1..4 prefill tile configs. */
+#define W4A16_VARIANT_AUTO   (-1)
+#define W4A16_VARIANT_DECODE 0
+#define W4A16_NUM_PREFILL_CFG 4
+
+/* Problem description.  Pointer values are used only for the 16-byte alignment check. */
+typedef struct w4a16_problem {
+    int64_t M, K, N;          /* x is [M, K]; scales is [groups, N]                     */
+    int64_t groups;           /* rows of scales (K / G)                                  */
+    int64_t wp_words;         /* number of int32 words in Wp (must be N*K/8)             */
+    const void* Wp;
+    const void* x;
+    const void* scales;
+} w4a16_problem;
+
+/* Device limits the selector uses.  Fill with w4a16_query_device, or by hand on the host
+ * (CPU tests inject small limits to exercise the "no configuration fits" path). */
+typedef struct w4a16_device_limits {
+    int32_t cu_count;             /* compute units (256 on MI355X)                      */
+    int32_t lds_bytes_per_block;  /* max LDS bytes one workgroup may allocate            */
+    int32_t max_threads_per_block;
+    int32_t gcn_arch;             /* e.g. 950 for gfx950; 0 = unknown                     */
+} w4a16_device_limits;
+
+/* A launch plan: the result of validation + routing + selection.  Plain data; copyable. */
+typedef struct w4a16_plan {
+    int32_t M, N, K, G;
+    int32_t kernel;           /* 0 = decode, 1..4 = prefill tile config                 */
+    int32_t splits;           /* decode: number of K slabs reduced across workgroups     */
+    int32_t slab_chunks;      /* decode: 64-wide K chunks per slab                       */
+    int32_t tile_n;           /* decode: output columns per workgroup                    */
+    int32_t grid;             /* workgroups launched by the main kernel                  */
+    int32_t block;            /* threads per workgroup                                   */
+    int32_t counter_slots;    /* ints of the counter buffer used (decode split-K fixup)  */
+    int32_t reserved;
+    uint64_t workspace_bytes; /* bytes of fp32 partials the launch needs (0 if none)     */
+} w4a16_plan;
+
+/* Validate a problem and build a plan.  Pure host code: touches no device.
+ * variant: -1 auto, 0 decode, 1..4 prefill config.  On failure returns W4A16_ERR_INVALID or
+ * W4A16_ERR_NO_CONFIG and writes the reference's error message into err (NUL-terminated).
+ * The messages (and their order) follow kernel.cu:224-249, 52, 196-198. */
+int w4a16_plan_create(const w4a16_problem* prob, int variant, const w4a16_device_limits* lim,
+                      w4a16_plan* plan, char* err, size_t errlen);
+
+/* Launch a plan on a HIP stream (asynchronous; no host synchronisation, no allocation, so it
+ * may be captured into a HIP graph).
+ *   workspace : device buffer of >= plan->workspace_bytes bytes (may be NULL when 0).
+ *   counters  : device int32 buffer of >= plan->counter_slots ints (may be NULL when 0).
+ *               It must be all-zero before the first launch that uses it; every launch leaves
+ *               it all-zero again.  Launches that share one counter buffer must not overlap
+ *               in time (use one buffer per concurrently running stream).
+ * Returns W4A16_OK or W4A16_ERR_HIP / W4A16_ERR_WORKSPACE. */
+int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
+                 const uint16_t* scales, uint16_t* y, void* workspace, int32_t* counters,
+                 void* stream);
+
+/* Query the limits of HIP device `device` (cached per device, thread-safe). */
+int w4a16_query_device(int device, w4a16_device_limits* lim);
+
+/* Largest counter_slots any plan may request (size of a counter buffer that fits all plans). */
+int32_t w4a16_max_counter_slots(void);
+
+/* Message of the last failing HIP call on this thread ("" if none). */
+const char* w4a16_last_error(void);
+
+/* ABI version (W4A16_ABI_VERSION). */
+int w4a16_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_H_ */

@@ -1,0 +1,349 @@
+"""GPU parity tests of the MI355X W4A16 op against the CPU oracle.
+
+Mirrors the contract of the reference suite (tests/test_w4a16.py, every test function, same
+parametrisations and tolerances) plus the BASELINE configurations.  The op is called through
+the PyTorch binding, which calls the C ABI of libw4a16_hip.so.  The expected values come from
+the oracle (oracle/quant.py: numpy restatement of tests/quant.py), computed on the host.
+
+    python -u -m pytest tests -m gpu -x -v --timeout 120 --timeout-method thread
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import quant
+from tests._helpers import (PKG, assert_close, dequant_f32, ext_module_path, gemm, make_problem,
+                            ref_gemm, torch_cuda)
+
+pytestmark = pytest.mark.gpu
+
+GS = [64, 128]
+DECODE_SHAPES = [
+    (64, 512), (128, 1024), (256, 2048), (512, 4096),
+    (4096, 4096), (6144, 4096), (4096, 14336), (28672, 4096),
+]
+DECODE_BATCHES = [1, 2, 3, 7, 8, 9, 15, 16]
+PREFILL_VARIANTS = [1, 2, 3, 4]
+PREFILL_M = [17, 31, 32, 33, 63, 64, 65, 100, 127, 128, 129, 300, 512, 1000]
+RAGGED = [(16, 64), (48, 192), (80, 640), (208, 384), (272, 1152)]
+
+
+def test_extension_is_in_tree_hip_build():
+    """The op must be the in-tree HIP build (no silent fallback)."""
+    torch_cuda()
+    import os
+    path = ext_module_path()
+    assert os.path.dirname(path) == os.path.realpath(PKG), path
+    import w4a16_opt
+    info = w4a16_opt.plan_info(1, 4096, 4096, 128)
+    assert info["gcn_arch"] == 950, info
+
+
+# ------------------------------------------------------------------ reference contract mirror
+
+@pytest.mark.parametrize("G", GS)
+@pytest.mark.parametrize("M", DECODE_BATCHES)
+@pytest.mark.parametrize("N,K", DECODE_SHAPES[:4])
+def test_shapes(M, N, K, G):
+    x, q, scales, Wp, key = make_problem(M, N, K, G)
+    assert_close(gemm(Wp, x, scales), ref_gemm(x, q, scales, G, key))
+
+
+@pytest.mark.parametrize("G", [128])
+@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("N,K", DECODE_SHAPES[4:])
+def test_llama3_8b_shapes(M, N, K, G):
+    x, q, scales, Wp, key = make_problem(M, N, K, G)
+    assert_close(gemm(Wp, x, scales), ref_gemm(x, q, scales, G, key))
+
+
+@pytest.mark.parametrize("G", GS)
+@pytest.mark.parametrize("M", PREFILL_M)
+@pytest.mark.parametrize("N,K", DECODE_SHAPES[:4])
+def test_prefill_auto(M, N, K, G):
+    x, q, scales, Wp, key = make_problem(M, N, K, G)
+    assert_close(gemm(Wp, x, scales), ref_gemm(x, q, scales, G, key))
+
+
+@pytest.mark.parametrize("G", GS)
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 70, 200])
+@pytest.mark.parametrize("N,K", RAGGED)
+def test_ragged_shapes_auto(M, N, K, G):
+    if K % G:
+        pytest.skip("K must be a multiple of the group size")
+    x, q, scales, Wp, key = make_problem(M, N, K, G)
+    assert_close(gemm(Wp, x, scales), ref_gemm(x, q, scales, G, key))
+
+
+@pytest.mark.parametrize("variant", PREFILL_VARIANTS)
+@pytest.mark.parametrize("G", GS)
+@pytest.mark.parametrize("M", [1, 7, 16, 17, 33, 129])
+@pytest.mark.parametrize("N,K", [(64, 512), (208, 384), (512, 4096)])
+def test_forced_prefill_variants(variant, M, N, K, G):
+    if K % G:
+        pytest.skip("K must be a multiple of the group size")
+    x, q, scales, Wp, key = make_problem(M, N, K, G)
+    assert_close(gemm(Wp, x, scales, variant=variant), ref_gemm(x, q, scales, G, key))
+
+
+@pytest.mark.parametrize("G", GS)
+def test_prefill_variants_bitwise_equal(G):
+    """Every prefill config accumulates K in the same order -> identical bits."""
+    torch = torch_cuda()
+    x, q, scales, Wp, key = make_problem(200, 384, 2048, G, seed=5)
+    ys = [gemm(Wp, x, scales, variant=v) for v in PREFILL_VARIANTS]
+    for y in ys[1:]:
+        assert torch.equal(ys[0], y)
+    assert_close(ys[0], ref_gemm(x, q, scales, G, key))
+
+
+@pytest.mark.parametrize("G", GS)
+def test_prefill_rows_independent_of_batch(G):
+    torch = torch_cuda()
+    x, q, scales, Wp, key = make_problem(150, 256, 1024, G, seed=9)
+    full = gemm(Wp, x, scales)
+    for m in (17, 40, 64, 99):
+        assert torch.equal(gemm(Wp, x[:m].contiguous(), scales), full[:m])
+
+
+@pytest.mark.parametrize("G", [128])
+@pytest.mark.parametrize("M", [17, 128, 1024])
+@pytest.mark.parametrize("N,K", DECODE_SHAPES[4:7])
+def test_llama3_8b_prefill_shapes(M, N, K, G):
+    x, q, scales, Wp, key = make_problem(M, N, K, G)
+    assert_close(gemm(Wp, x, scales), ref_gemm(x, q, scales, G, key))
+
+
+def test_decode_variant_matches_prefill():
+    x, q, scales, Wp, key = make_problem(8, 1024, 2048, 128)
+    ref = ref_gemm(x, q, scales, 128, key)
+    assert_close(gemm(Wp, x, scales, variant=0), ref)
+    assert_close(gemm(Wp, x, scales, variant=3), ref)
+
+
+def test_decode_variant_rejects_unsupported_shapes():
+    x, q, scales, Wp, key = make_problem(32, 64, 512, 64)
+    with pytest.raises(RuntimeError, match="decode kernel needs"):
+        gemm(Wp, x, scales, variant=0)
+    x, q, scales, Wp, key = make_problem(4, 80, 640, 64)
+    with pytest.raises(RuntimeError, match="decode kernel needs"):
+        gemm(Wp, x, scales, variant=0)
+
+
+@pytest.mark.parametrize("G", GS)
+@pytest.mark.parametrize("scale_mode", ["tiny", "large", "mixed"])
+def test_hard_scale_and_activation_ranges(G, scale_mode):
+    M, N, K = 16, 256, 2048
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=23)
+    if scale_mode == "tiny":
+        scales.fill_(2.0 ** -14)
+        x.mul_(128)
+    elif scale_mode == "large":
+        scales.fill_(16.0)
+        x.mul_(8)
+    else:
+        scales[:, ::2] = 2.0 ** -10
+        scales[:, 1::2] = 8.0
+        x[::2].mul_(0.125)
+        x[1::2].mul_(8)
+    ref = ref_gemm(x, q, scales, G)
+    for v in [-1, 0] + PREFILL_VARIANTS:
+        assert_close(gemm(Wp, x, scales, variant=v), ref, tol=4e-3)
+
+
+@pytest.mark.parametrize("G", GS)
+def test_onehot_k_mapping(G):
+    """x = e_k -> y equals column k of the dequantised W exactly (reference :221-236)."""
+    torch = torch_cuda()
+    N, K = 128, 1024
+    _, q, scales, Wp, key = make_problem(1, N, K, G)
+    Wd = quant.dequantize_w4(q, scales.cpu().numpy(), G)
+    ks = [0, 1, 2, 7, 8, 15, 16, 17, 63, 64, 65, 127, 128, 255, 256, 511, 512, 513, 1022, 1023]
+    for i in range(0, len(ks), 16):
+        chunk = ks[i:i + 16]
+        x = torch.zeros(len(chunk), K, dtype=torch.half, device="cuda")
+        for m, k in enumerate(chunk):
+            x[m, k] = 1
+        want = np.ascontiguousarray(Wd[:, chunk].T)
+        for v in [-1, 0] + PREFILL_VARIANTS:
+            y = gemm(Wp, x, scales, variant=v).cpu().numpy()
+            assert np.array_equal(y.view(np.uint16), want.view(np.uint16)), \
+                f"k-mapping wrong for k in {chunk}, variant {v}"
+
+
+@pytest.mark.parametrize("fill", ["zeros", "fifteens", "random"])
+def test_nibble_extremes(fill):
+    torch = torch_cuda()
+    M, N, K, G = 4, 128, 1024, 64
+    rng = np.random.default_rng(1)
+    q = {"zeros": np.zeros((N, K), np.uint8),
+         "fifteens": np.full((N, K), 15, np.uint8),
+         "random": rng.integers(0, 16, (N, K), dtype=np.uint8)}[fill]
+    scales = (rng.random((K // G, N)) * 0.05 + 0.001).astype(np.float16)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    Wp = torch.from_numpy(quant.pack_int4(q)).cuda()
+    xt, st = torch.from_numpy(x).cuda(), torch.from_numpy(scales).cuda()
+    for v in [-1, 0] + PREFILL_VARIANTS:
+        assert_close(gemm(Wp, xt, st, variant=v), quant.ref_gemm(x, q, scales, G))
+
+
+def test_zero_input():
+    torch = torch_cuda()
+    x, q, scales, Wp, key = make_problem(5, 128, 1024, 64)
+    for v in [-1, 0] + PREFILL_VARIANTS:
+        assert not gemm(Wp, torch.zeros_like(x), scales, variant=v).any()
+
+
+def test_deterministic():
+    torch = torch_cuda()
+    x, q, scales, Wp, key = make_problem(8, 1024, 2048, 128)
+    assert torch.equal(gemm(Wp, x, scales), gemm(Wp, x, scales))
+    for v in PREFILL_VARIANTS:
+        assert torch.equal(gemm(Wp, x, scales, variant=v), gemm(Wp, x, scales, variant=v))
+
+
+@pytest.mark.parametrize("M", [1, 12, 40, 300])
+def test_cuda_graph_capture(M):
+    """Graph capture and replay (reference :264-278), replayed several times with eager work and
+    synchronisation between replays; every replay is checked."""
+    torch = torch_cuda()
+    x, q, scales, Wp, key = make_problem(M, 512, 1024, 128)
+    gemm(Wp, x, scales)                                   # warm up (creates decode counters)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = gemm(Wp, x, scales)
+    for rep in range(3):
+        x2 = torch.randn(x.shape, device="cuda").half()
+        x.copy_(x2)
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(y, ref_gemm(x2, q, scales, 128, key))
+        eager = gemm(Wp, x2, scales)
+        torch.cuda.synchronize()
+        assert torch.equal(eager, y), f"replay {rep} differs from the eager result"
+
+
+def test_rejects_bad_inputs():
+    torch = torch_cuda()
+
+    def args(**kw):
+        p = dict(M=2, N=64, K=512, G=64)
+        p.update(kw)
+        x, q, s, Wp, key = make_problem(p["M"], p["N"], p["K"], p["G"])
+        return Wp, x, s
+
+    Wp, x, s = args()
+    with pytest.raises(RuntimeError, match="fp16"):
+        gemm(Wp, x.float(), s)
+    with pytest.raises(RuntimeError, match="int32"):
+        gemm(Wp.to(torch.int64), x, s)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        gemm(Wp.cpu(), x.cpu(), s.cpu())
+    with pytest.raises(RuntimeError, match="contiguous"):
+        gemm(Wp, torch.empty(512, 2, dtype=torch.half, device="cuda").t(), s)
+    with pytest.raises(RuntimeError, match="variant"):
+        gemm(Wp, x, s, variant=7)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        gemm(Wp[: 64 * 32 // 8], torch.zeros(2, 32, dtype=torch.half, device="cuda"), s[:1, :64].contiguous())
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        gemm(Wp[: 24 * 512 // 8], x, s[:, :24].contiguous())
+    with pytest.raises(RuntimeError, match="unsupported group size"):
+        gemm(*args(G=32))
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        gemm(Wp, torch.zeros(2 * 512 + 1, dtype=torch.half, device="cuda")[1:].view(2, 512), s)
+    with pytest.raises(RuntimeError, match="N\\*K/8"):
+        gemm(Wp[:-4], x, s)
+
+
+# ----------------------------------------------------------------- beyond the reference suite
+
+@pytest.mark.parametrize("G", GS)
+def test_onehot_every_k(G):
+    """Exhaustive k mapping on a small shape: e_k for every k, all kernels, bit-exact."""
+    torch = torch_cuda()
+    N, K = 64, 512
+    _, q, scales, Wp, key = make_problem(1, N, K, G, seed=3)
+    Wd = quant.dequantize_w4(q, scales.cpu().numpy(), G)
+    for k0 in range(0, K, 16):
+        x = torch.zeros(16, K, dtype=torch.half, device="cuda")
+        x[torch.arange(16), torch.arange(k0, k0 + 16)] = 1
+        want = np.ascontiguousarray(Wd[:, k0:k0 + 16].T)
+        for v in [0] + PREFILL_VARIANTS:
+            y = gemm(Wp, x, scales, variant=v).cpu().numpy()
+            assert np.array_equal(y.view(np.uint16), want.view(np.uint16)), (k0, v)
+
+
+def test_subnormal_scales_bit_exact():
+    """fp16 subnormal products must not be flushed: one-hot columns with scales 2^-20..2^-15."""
+    torch = torch_cuda()
+    N, K, G = 128, 512, 64
+    rng = np.random.default_rng(7)
+    q = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    scales = (2.0 ** rng.integers(-24, -14, (K // G, N))).astype(np.float16)
+    Wd = quant.dequantize_w4(q, scales, G)
+    assert (np.abs(Wd.astype(np.float32)) < 2.0 ** -14).any()
+    Wp = torch.from_numpy(quant.pack_int4(q)).cuda()
+    st = torch.from_numpy(scales).cuda()
+    for k0 in (0, 37, 255, 496):
+        x = torch.zeros(16, K, dtype=torch.half, device="cuda")
+        x[torch.arange(16), torch.arange(k0, k0 + 16)] = 1
+        want = np.ascontiguousarray(Wd[:, k0:k0 + 16].T)
+        for v in [0] + PREFILL_VARIANTS:
+            y = gemm(Wp, x, st, variant=v).cpu().numpy()
+            assert np.array_equal(y.view(np.uint16), want.view(np.uint16)), (k0, v)
+
+
+def _baseline_problem(M, N, K, G, seed, ragged=False):
+    torch = torch_cuda()
+    if ragged:
+        q, scales = quant.gen_codes_scales(N, K, G, seed, 1e-4, 0.05)
+        rng = np.random.default_rng([seed, 2])
+        xf = rng.standard_normal((M, K)) * 2.0
+        mask = rng.random((M, K)) < 0.01
+        xf[mask] = np.where(rng.random(mask.sum()) < 0.5, -60.0, 60.0)
+        x = xf.astype(np.float16)
+    else:
+        q, scales = quant.gen_codes_scales(N, K, G, seed)
+        x = np.random.default_rng([seed, 2]).standard_normal((M, K)).astype(np.float16)
+    Wp = quant.pack_int4(q)
+    return (torch.from_numpy(x).cuda(), torch.from_numpy(scales).cuda(), torch.from_numpy(Wp).cuda(),
+            x, q, scales)
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2_gate_up_1", "c2_gate_up_16", "c2_down_4", "c2_down_8", "c3"])
+def test_baseline_configs(cfg):
+    """BASELINE.json configs 1-3 with their stated distributions, against the oracle."""
+    spec = {"c1": (1, 4096, 4096, 128), "c2_gate_up_1": (1, 14336, 4096, 128),
+            "c2_gate_up_16": (16, 14336, 4096, 128), "c2_down_4": (4, 4096, 14336, 128),
+            "c2_down_8": (8, 4096, 14336, 128), "c3": (128, 14336, 4096, 64)}[cfg]
+    M, N, K, G = spec
+    xt, st, Wt, x, q, scales = _baseline_problem(M, N, K, G, seed=11)
+    ref = quant.ref_gemm(x, q, scales, G)
+    assert_close(gemm(Wt, xt, st), ref)
+    if cfg == "c3":
+        import torch
+        ys = [gemm(Wt, xt, st, variant=v) for v in PREFILL_VARIANTS]
+        for y in ys[1:]:
+            assert torch.equal(ys[0], y)
+
+
+@pytest.mark.parametrize("G", [64])
+def test_baseline_c5_ragged_rows_independent(G):
+    """Config 5: N=4112 (N%64 != 0), K=4160, 65 groups, outliers; rows independent of M."""
+    torch = torch_cuda()
+    N, K = 4112, 4160
+    xt, st, Wt, x, q, scales = _baseline_problem(513, N, K, G, seed=13, ragged=True)
+    full = gemm(Wt, xt, st)
+    assert_close(full, quant.ref_gemm(x, q, scales, G))
+    for m in (1, 17, 37, 100):
+        assert torch.equal(gemm(Wt, xt[:m].contiguous(), st), full[:m]), m
+
+
+def test_decode_split_consistency_large_k():
+    """Decode at K=14336 (many K slabs) vs prefill on the same inputs: both within tolerance."""
+    x, q, scales, Wp, key = make_problem(16, 4096, 14336, 128, seed=4)
+    ref = ref_gemm(x, q, scales, 128, key)
+    assert_close(gemm(Wp, x, scales, variant=0), ref)
+    assert_close(gemm(Wp, x, scales, variant=2), ref)

@@ -1,0 +1,89 @@
+"""Build the MI355X W4A16 library and its PyTorch binding in-tree.
+
+    python w4a16-gemm_amd/build.py            # builds both
+    python w4a16-gemm_amd/build.py --lib      # only libw4a16_hip.so
+
+Outputs (next to this file, git-ignored, shipped to the GPU box with the tree):
+  libw4a16_hip.so              hipcc --offload-arch=gfx950: kernels + C ABI (include/w4a16.h)
+  w4a16_opt<EXT_SUFFIX>        host-compiler (g++) PyTorch extension linking libw4a16_hip.so
+                               through an $ORIGIN rpath; import it as `w4a16_opt`.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+LIB = os.path.join(HERE, "libw4a16_hip.so")
+EXT = os.path.join(HERE, "w4a16_opt" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+# gfx950 only; packed-fp32 VALU ops disabled for all device code (-packed-fp32-ops).
+HIPCC_FLAGS = [
+    "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    print("+", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines()
+                    if "packed-fp32-ops" not in l and "target-feature" not in l)
+    if out.strip():
+        print(out, flush=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
+
+
+def build_lib() -> str:
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    srcs = [os.path.join(CSRC, "w4a16_kernels.hip"), os.path.join(CSRC, "w4a16_plan.cpp")]
+    tmp = LIB + ".tmp"
+    _run([hipcc, *HIPCC_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_ext() -> str:
+    import torch.utils.cpp_extension as ce
+    import torch
+
+    cxx = os.environ.get("CXX", "g++")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [INCLUDE, *ce.include_paths(), sysconfig.get_paths()["include"], os.path.join(ROCM, "include")]
+    libdirs = [*ce.library_paths(), os.path.join(ROCM, "lib"), HERE]
+    tmp = EXT + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=w4a16_opt",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-Wno-deprecated-declarations",
+           *[f"-I{p}" for p in incs],
+           os.path.join(CSRC, "w4a16_torch.cpp"),
+           *[f"-L{p}" for p in libdirs],
+           "-lw4a16_hip", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+           "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    _run(cmd)
+    os.replace(tmp, EXT)
+    return EXT
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--lib", action="store_true", help="only build libw4a16_hip.so")
+    a = ap.parse_args(argv)
+    build_lib()
+    if not a.lib:
+        build_ext()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,204 @@
+// Host-side validation, routing and tile selection for the W4A16 GEMM (pure host code: the
+// planner touches no device, so it is unit-tested on CPU through the C ABI).
+//
+// Validation order and message text follow the reference op w4a16_gemm_cuda
+// (src/vectorized/kernel.cu:224-249); the tensor-level checks that precede them in the
+// reference (device, contiguity, dtypes, ranks: kernel.cu:219-223) live in the torch binding,
+// which owns the tensors.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "w4a16.h"
+#include "w4a16_internal.h"
+
+using namespace w4a16;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, char* err, size_t errlen, const char* fmt, ...) {
+    if (err && errlen) {
+        va_list ap;
+        va_start(ap, fmt);
+        std::vsnprintf(err, errlen, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+bool debug_enabled() {
+    static const bool on = std::getenv("W4A16_DEBUG_PREFILL") != nullptr;
+    return on;
+}
+
+// LDS per CU: 160 KB on gfx950 (CDNA4), 64 KB on earlier CDNA parts.
+int lds_per_cu(const w4a16_device_limits& lim) {
+    return lim.gcn_arch >= 950 ? 160 * 1024 : 64 * 1024;
+}
+
+// Resident workgroups per CU for a prefill config (LDS- and wave-slot-limited estimate;
+// registers are budgeted so that two workgroups of any config fit).
+int prefill_occupancy(int cfg, const w4a16_device_limits& lim) {
+    const int lds = prefill_lds_bytes(cfg);
+    if (lds > lim.lds_bytes_per_block) return 0;
+    if (prefill_threads(cfg) > lim.max_threads_per_block) return 0;
+    int occ = lds_per_cu(lim) / lds;
+    const int waves = kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n;
+    occ = std::min(occ, 32 / waves);      // 8 wave slots per SIMD x 4 SIMDs
+    occ = std::min(occ, 2);               // VGPR budget (acc + operands) of the larger tiles
+    return occ;
+}
+
+// Auto prefill selection (replaces pf_select, kernel.cu:142-156).  Cost = full-device waves of
+// tiles x per-wave work, where a tile's work is BN * (BM + 32): the MFMA work plus the
+// per-tile dequantisation overhead, which is paid once per weight column block and wave row.
+int prefill_select(int M, int N, const w4a16_device_limits& lim) {
+    int best = 0;
+    double best_cost = std::numeric_limits<double>::infinity();
+    const double cus = lim.cu_count > 0 ? lim.cu_count : 1;
+    for (int cfg = kNumPrefillCfg; cfg >= 1; --cfg) {      // descending: ties go to larger BM
+        const int occ = prefill_occupancy(cfg, lim);
+        if (occ < 1) continue;
+        const PrefillTile& t = kPrefillTable[cfg];
+        const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
+        if (tiles > (double)std::numeric_limits<int32_t>::max()) continue;
+        const double waves = std::ceil(tiles / (cus * occ));
+        const double cost = waves * occ * t.bn * (t.bm + 32.0);
+        if (cost < best_cost) { best_cost = cost; best = cfg; }
+    }
+    return best;
+}
+
+}  // namespace
+
+extern "C" void w4a16_set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
+extern "C" const char* w4a16_last_error(void) { return g_last_error.c_str(); }
+extern "C" int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
+extern "C" int32_t w4a16_max_counter_slots(void) { return kMaxCounterSlots; }
+
+extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w4a16_device_limits* lim,
+                                 w4a16_plan* plan, char* err, size_t errlen) {
+    if (err && errlen) err[0] = '\0';
+    if (!prob || !lim || !plan) return fail(W4A16_ERR_INVALID, err, errlen, "null argument");
+    const w4a16_problem& p = *prob;
+
+    // kernel.cu:224-240, in the same order and with the same messages.
+    if (variant < -1 || variant > kNumPrefillCfg)
+        return fail(W4A16_ERR_INVALID, err, errlen, "variant must be -1 (auto), 0 (decode) or 1..%d", kNumPrefillCfg);
+    if (p.M < 1) return fail(W4A16_ERR_INVALID, err, errlen, "M must be at least 1");
+    const int64_t lim32 = (int64_t)1 << 31;
+    if (!(p.M < lim32 && p.K < lim32 && p.N < lim32) || p.K < 0 || p.N < 0)
+        return fail(W4A16_ERR_INVALID, err, errlen, "dimensions must fit in int32");
+    const int M = (int)p.M, K = (int)p.K, N = (int)p.N;
+    if (K % 64 != 0) return fail(W4A16_ERR_INVALID, err, errlen, "K must be a multiple of 64");
+    if (N % 16 != 0) return fail(W4A16_ERR_INVALID, err, errlen, "N must be a multiple of 16");
+    if (!(p.groups > 0 && K % p.groups == 0))
+        return fail(W4A16_ERR_INVALID, err, errlen, "K must be divisible by the number of groups");
+    if (p.wp_words != (int64_t)N * K / 8) return fail(W4A16_ERR_INVALID, err, errlen, "Wp must hold N*K/8 words");
+    if ((reinterpret_cast<uintptr_t>(p.Wp) | reinterpret_cast<uintptr_t>(p.x) |
+         reinterpret_cast<uintptr_t>(p.scales)) % 16 != 0)
+        return fail(W4A16_ERR_INVALID, err, errlen, "Wp, x and scales must be 16-byte aligned");
+    const int G = K / (int)p.groups;
+    if (G != 64 && G != 128)
+        return fail(W4A16_ERR_INVALID, err, errlen, "unsupported group size %d, supported: 64, 128", G);
+
+    // Routing (kernel.cu:242-249): the decode kernel keeps its shape contract.
+    const bool decode_ok = (M <= 16) && (N % 64 == 0) && (K % 512 == 0);
+    int v = variant;
+    if (v == -1 && decode_ok) v = 0;
+    if (v == 0 && !decode_ok)
+        return fail(W4A16_ERR_INVALID, err, errlen,
+                    "decode kernel needs M in [1, 16], N a multiple of 64 and K a multiple of 512 "
+                    "(use variant=-1 or 1..4 for other shapes)");
+
+    w4a16_plan out;
+    std::memset(&out, 0, sizeof(out));
+    out.M = M; out.N = N; out.K = K; out.G = G;
+
+    if (v == 0) {
+        // Decode: 64-column tiles x K slabs of KS chunks.  Pick the largest slab that still
+        // gives >= 4 workgroups per CU (memory-level parallelism); otherwise the smallest slab.
+        const int KC = K / 64;
+        const int ntiles = N / kDecodeTileN;
+        const int cus = lim->cu_count > 0 ? lim->cu_count : 1;
+        const int cand[3] = {16, 8, 4};
+        int ks = 0;
+        for (int i = 0; i < 3; ++i) {
+            const int c = cand[i];
+            if (KC % c || decode_lds_bytes(c) > lim->lds_bytes_per_block) continue;
+            if (kDecodeWaves * 64 > lim->max_threads_per_block) continue;
+            ks = c;                                           // smallest valid so far
+            if ((int64_t)ntiles * (KC / c) >= 4LL * cus) break;
+        }
+        if (!ks)
+            return fail(W4A16_ERR_NO_CONFIG, err, errlen, "no pipeline configuration fits in %d B of shared memory",
+                        lim->lds_bytes_per_block);
+        int splits = KC / ks;
+        if (ntiles > kMaxCounterSlots) { ks = 0; }
+        if (!ks) return fail(W4A16_ERR_NO_CONFIG, err, errlen, "N too large for the decode kernel");
+        out.kernel = 0;
+        out.slab_chunks = ks;
+        out.splits = splits;
+        out.tile_n = kDecodeTileN;
+        out.block = kDecodeWaves * 64;
+        out.grid = ntiles * splits;
+        out.counter_slots = splits > 1 ? ntiles : 0;
+        out.workspace_bytes = splits > 1 ? (uint64_t)splits * M * N * sizeof(float) : 0;
+        if (debug_enabled())
+            std::fprintf(stderr, "decode dispatch G=%d M=%d N=%d K=%d slab=%d splits=%d grid=%d\n",
+                         G, M, N, K, ks, splits, out.grid);
+    } else {
+        int cfg = v;                                          // 1..4 forced, or -1 = auto
+        if (cfg < 0) cfg = prefill_select(M, N, *lim);
+        if (!(cfg >= 1 && cfg <= kNumPrefillCfg && prefill_occupancy(cfg, *lim) > 0))
+            return fail(W4A16_ERR_NO_CONFIG, err, errlen,
+                        "no prefill configuration fits (shared memory limit %d B, M=%d)", lim->lds_bytes_per_block, M);
+        const PrefillTile& t = kPrefillTable[cfg];
+        const int64_t tiles = ((int64_t)(M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+        if (tiles > std::numeric_limits<int32_t>::max())
+            return fail(W4A16_ERR_INVALID, err, errlen, "M too large for prefill config %d", cfg);
+        out.kernel = cfg;
+        out.block = prefill_threads(cfg);
+        out.grid = (int32_t)tiles;
+        if (debug_enabled())
+            std::fprintf(stderr, "prefill dispatch G=%d M=%d N=%d K=%d cfg=%d occ=%d tiles=%d\n",
+                         G, M, N, K, cfg, prefill_occupancy(cfg, *lim), out.grid);
+    }
+    *plan = out;
+    return W4A16_OK;
+}
+
+extern "C" int w4a16_query_device(int device, w4a16_device_limits* lim) {
+    static std::mutex mu;
+    static std::map<int, w4a16_device_limits> cache;
+    if (!lim) return W4A16_ERR_INVALID;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(device);
+    if (it != cache.end()) { *lim = it->second; return W4A16_OK; }
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        w4a16_set_last_error(hipGetErrorString(e));
+        return W4A16_ERR_HIP;
+    }
+    w4a16_device_limits l;
+    l.cu_count = prop.multiProcessorCount;
+    l.lds_bytes_per_block = (int32_t)prop.sharedMemPerBlock;
+    l.max_threads_per_block = prop.maxThreadsPerBlock;
+    l.gcn_arch = 0;
+    const char* a = prop.gcnArchName;                      // e.g. "gfx950:sramecc+:xnack-"
+    if (a && std::strncmp(a, "gfx", 3) == 0) l.gcn_arch = (int32_t)std::strtol(a + 3, nullptr, 10);
+    cache[device] = l;
+    *lim = l;
+    return W4A16_OK;
+}

@@ -1,0 +1,131 @@
+// PyTorch-ROCm binding: module `w4a16_opt`, function `w4a16_gemm(Wp, x, scales, variant=-1)`.
+//
+// Drop-in for the reference's pybind11 entry point (src/vectorized/extension.cpp:5-9) and the
+// tensor-level half of w4a16_gemm_cuda (src/vectorized/kernel.cu:218-267).  All numeric
+// validation, routing, tile selection and the kernel launches go through the C ABI of
+// libw4a16_hip.so (include/w4a16.h); this file only owns tensors, the device guard, the current
+// stream, the output allocation and the split-K scratch.
+//
+// Compiled by the host compiler (no hipify, no device code).
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
+
+#include <map>
+#include <mutex>
+
+#include "w4a16.h"
+
+namespace {
+
+// Per-device decode split-K counters.  Zeroed once when created; every decode launch leaves
+// them zero again (w4a16.h).  Creating them allocates and fills, so the first decode call on
+// a device must not be inside HIP graph capture (the reference likewise expects one eager
+// call before capture: tests/test_w4a16.py:269).
+std::mutex g_mu;
+std::map<int, at::Tensor> g_counters;
+
+int32_t* decode_counters(const at::Tensor& like, hipStream_t stream) {
+    const int dev = like.device().index();
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_counters.find(dev);
+    if (it == g_counters.end()) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        TORCH_CHECK(hipStreamIsCapturing(stream, &st) == hipSuccess, "hipStreamIsCapturing failed");
+        TORCH_CHECK(st == hipStreamCaptureStatusNone,
+                    "w4a16_gemm: the first decode call on a device must run outside graph capture "
+                    "(it creates the split-K counter buffer); call it once eagerly before capturing");
+        at::Tensor t = torch::zeros({(int64_t)w4a16_max_counter_slots()},
+                                    like.options().dtype(torch::kInt32));
+        it = g_counters.emplace(dev, t).first;
+    }
+    return it->second.data_ptr<int32_t>();
+}
+
+w4a16_device_limits limits_for(int dev) {
+    w4a16_device_limits lim;
+    const int rc = w4a16_query_device(dev, &lim);
+    TORCH_CHECK(rc == W4A16_OK, "w4a16_gemm: device query failed: ", w4a16_last_error());
+    return lim;
+}
+
+}  // namespace
+
+torch::Tensor w4a16_gemm(torch::Tensor Wp, torch::Tensor x, torch::Tensor scales, int64_t variant) {
+    // kernel.cu:219-223 (same order, same messages; ROCm tensors report is_cuda()).
+    TORCH_CHECK(Wp.is_cuda() && x.is_cuda() && scales.is_cuda(), "all tensors must be CUDA");
+    TORCH_CHECK(Wp.is_contiguous() && x.is_contiguous() && scales.is_contiguous(), "contiguous only");
+    TORCH_CHECK(Wp.dtype() == torch::kInt32, "Wp must be int32");
+    TORCH_CHECK(x.dtype() == torch::kHalf && scales.dtype() == torch::kHalf, "x, scales must be fp16");
+    TORCH_CHECK(x.dim() == 2 && scales.dim() == 2, "x must be [M, K], scales must be [K/G, N]");
+
+    w4a16_problem prob;
+    prob.M = x.size(0);
+    prob.K = x.size(1);
+    prob.N = scales.size(1);
+    prob.groups = scales.size(0);
+    prob.wp_words = Wp.numel();
+    prob.Wp = Wp.data_ptr();
+    prob.x = x.data_ptr();
+    prob.scales = scales.data_ptr();
+
+    const c10::DeviceGuard guard(x.device());
+    const int dev = x.device().index();
+    const w4a16_device_limits lim = limits_for(dev);
+    w4a16_plan plan;
+    char err[512];
+    const int rc = w4a16_plan_create(&prob, (int)std::max<int64_t>(std::min<int64_t>(variant, 1 << 20), -(1 << 20)),
+                                     &lim, &plan, err, sizeof(err));
+    TORCH_CHECK(rc == W4A16_OK, err);
+    TORCH_CHECK(Wp.device() == x.device() && scales.device() == x.device(),
+                "Wp, x and scales must be on the same device");
+
+    hipStream_t stream = c10::hip::getCurrentHIPStream(dev).stream();
+    torch::Tensor y = torch::empty({prob.M, prob.N}, x.options());
+    if (y.numel() == 0) return y;
+
+    torch::Tensor ws;
+    void* ws_ptr = nullptr;
+    if (plan.workspace_bytes) {
+        ws = torch::empty({(int64_t)plan.workspace_bytes}, x.options().dtype(torch::kUInt8));
+        ws_ptr = ws.data_ptr();
+    }
+    int32_t* cnt = plan.counter_slots ? decode_counters(x, stream) : nullptr;
+
+    const int lrc = w4a16_launch(&plan, static_cast<const int32_t*>(prob.Wp),
+                                 static_cast<const uint16_t*>(prob.x), static_cast<const uint16_t*>(prob.scales),
+                                 reinterpret_cast<uint16_t*>(y.data_ptr()), ws_ptr, cnt, stream);
+    TORCH_CHECK(lrc == W4A16_OK, "w4a16_gemm: launch failed (code ", lrc, "): ", w4a16_last_error());
+    return y;
+}
+
+// Introspection used by the tests and the benchmark: the plan the op would launch.
+py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t variant, int64_t device) {
+    w4a16_problem prob;
+    prob.M = M; prob.N = N; prob.K = K;
+    prob.groups = G > 0 ? K / G : 0;
+    prob.wp_words = N * K / 8;
+    prob.Wp = prob.x = prob.scales = nullptr;
+    const w4a16_device_limits lim = limits_for((int)device);
+    w4a16_plan plan;
+    char err[512];
+    const int rc = w4a16_plan_create(&prob, (int)variant, &lim, &plan, err, sizeof(err));
+    TORCH_CHECK(rc == W4A16_OK, err);
+    py::dict d;
+    d["kernel"] = plan.kernel; d["splits"] = plan.splits; d["slab_chunks"] = plan.slab_chunks;
+    d["tile_n"] = plan.tile_n; d["grid"] = plan.grid; d["block"] = plan.block;
+    d["counter_slots"] = plan.counter_slots; d["workspace_bytes"] = (uint64_t)plan.workspace_bytes;
+    d["cu_count"] = lim.cu_count; d["gcn_arch"] = lim.gcn_arch; d["lds_bytes_per_block"] = lim.lds_bytes_per_block;
+    return d;
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("w4a16_gemm", &w4a16_gemm,
+          "W4A16 group-wise GEMM on MI355X MFMA (decode M<=16 split-K kernel + tiled prefill for any M)",
+          py::arg("Wp"), py::arg("x"), py::arg("scales"), py::arg("variant") = -1);
+    m.def("plan_info", &w4a16_plan_info, "Plan the op would launch for a shape (debug / bench)",
+          py::arg("M"), py::arg("N"), py::arg("K"), py::arg("G"), py::arg("variant") = -1, py::arg("device") = 0);
+    m.attr("abi_version") = w4a16_abi_version();
+}
