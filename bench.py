@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W4A16 GEMM on BASELINE.json's metric.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill]
+                    [--no-cpu] [--no-prefill] [--json PATH]
+
+Headline (default): decode GB/s on the Llama-3-8B MLP shapes,
+gate/up (K=4096, N=14336) and down (K=14336, N=4096) at M = 1, 4, 8, 16, G = 128.  One
+"step" is one call of the op for each of those 8 (shape, M) cases.  Weights rotate through
+enough copies that the working set (>= 720 MB) exceeds twice the 256 MB Infinity Cache, so
+every call streams its weights from HBM; x, scales and weights are resident in HBM before the
+timed region.  The calls are captured in HIP graphs (as the reference benchmark does with CUDA
+graphs, benchmarks/bench_gemm.py:36-56) and timed with HIP events on the launch stream.
+
+Second leg: prefill TFLOP/s at M=2048, K=8192, N=28672, G=128.
+
+Algorithmic work (the roofline numerator): bytes = N*K/2 + (K/G)*N*2 + M*K*2 + M*N*2 per call,
+flops = 2*M*N*K per call.  Peaks: HBM 8000 GB/s, fp16 dense MFMA 2500 TFLOP/s (MI355X spec).
+
+The CPU baseline times the oracle's C restatement of the reference CPU path (unpack + fp16
+dequant + fp32 GEMM, oracle/w4a16_oracle.c) on the host on a bounded sample of the same cases.
+Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "w4a16-gemm_amd")
+sys.path.insert(0, ROOT)
+sys.path.insert(0, PKG)
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFS = 2500.0
+MALL_BYTES = 256 * 2**20
+
+DECODE_CASES = [("gate_up", 14336, 4096, m) for m in (1, 4, 8, 16)] + \
+               [("down", 4096, 14336, m) for m in (1, 4, 8, 16)]
+PREFILL_CASE = ("mlp70b", 28672, 8192, 2048)
+G = 128
+
+
+def alg_bytes(M, N, K, G=G):
+    return N * K // 2 + (K // G) * N * 2 + M * K * 2 + M * N * 2
+
+
+def alg_flops(M, N, K):
+    return 2 * M * N * K
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_weights(torch, N, K, seed, copies):
+    """BASELINE distributions: q ~ U{0..15} packed in the reference layout, scales ~ U[0.002, 0.02].
+    The packing runs once on the host (oracle.quant.pack_int4 is only data preparation here); the
+    copies are device clones."""
+    from oracle import quant
+    q, scales = quant.gen_codes_scales(N, K, G, seed)
+    Wp = torch.from_numpy(quant.pack_int4(q)).cuda()
+    s = torch.from_numpy(scales).cuda()
+    return [(Wp, s)] + [(Wp.clone(), s.clone()) for _ in range(copies - 1)]
+
+
+def graph_of(torch, fn_list):
+    for f in fn_list:
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fn_list:
+            f()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, graphs, steps, warmup):
+    """Replay graphs[i % len] for warmup then exactly `steps` timed steps; HIP events on the
+    current stream (where the op launches).  Returns elapsed ms of the timed region."""
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end)
+
+
+def bench_decode(torch, gemm, steps, warmup):
+    copies = 12                                    # per shape: 2 x 12 x ~30 MB = 720 MB > 2 x MALL
+    w = {"gate_up": make_weights(torch, 14336, 4096, 101, copies),
+         "down": make_weights(torch, 4096, 14336, 102, copies)}
+    xs = {(name, M): torch.randn(M, K, device="cuda").half() for name, N, K, M in DECODE_CASES}
+    per_shape = 4                                  # calls per shape per step
+    phases = copies // per_shape                   # distinct copy rotations
+    graphs, ys = [], []
+    for ph in range(phases):
+        calls = []
+        for name, N, K, M in DECODE_CASES:
+            idx = ph * per_shape + [c[3] for c in DECODE_CASES if c[0] == name].index(M)
+            Wp, s = w[name][idx]
+            x = xs[(name, M)]
+            calls.append(lambda Wp=Wp, s=s, x=x: ys.append(gemm(Wp, x, s)))
+        graphs.append(graph_of(torch, calls))
+    # per-case timing (each case alone, rotating over all its copies)
+    cases = []
+    for name, N, K, M in DECODE_CASES:
+        x = xs[(name, M)]
+        g = graph_of(torch, [lambda Wp=Wp, s=s: gemm(Wp, x, s) for Wp, s in w[name]])
+        reps = []
+        for _ in range(5):
+            reps.append(time_graph(torch, [g], 4, 1) / (4 * copies))
+        us = statistics.median(reps) * 1e3
+        b = alg_bytes(M, N, K)
+        cases.append({"layer": name, "M": M, "N": N, "K": K, "us": round(us, 3),
+                      "GBps": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)})
+        log(f"decode {name} M={M}: {us:.2f} us  {b / us / 1e3:.0f} GB/s")
+    ms = time_graph(torch, graphs, steps, warmup)
+    step_bytes = sum(alg_bytes(M, N, K) for _, N, K, M in DECODE_CASES)
+    ms_per_step = ms / steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    avg_launch_us = ms_per_step * 1e3 / len(DECODE_CASES)
+    return {"value": value, "ms_per_step": ms_per_step, "step_bytes": step_bytes,
+            "avg_launch_us": avg_launch_us, "bytes_per_launch": step_bytes / len(DECODE_CASES),
+            "cases": cases, "copies": copies}
+
+
+def bench_prefill(torch, gemm, steps, warmup):
+    name, N, K, M = PREFILL_CASE
+    copies = 3                                     # 3 x 121 MB of weights + scales > MALL
+    w = make_weights(torch, N, K, 103, copies)
+    x = torch.randn(M, K, device="cuda").half()
+    graphs = [graph_of(torch, [lambda Wp=Wp, s=s: gemm(Wp, x, s)]) for Wp, s in w]
+    ms = time_graph(torch, graphs, steps, warmup)
+    us = ms * 1e3 / steps
+    tfs = alg_flops(M, N, K) / (us * 1e-6) / 1e12
+    log(f"prefill {name} M={M}: {us:.1f} us  {tfs:.1f} TFLOP/s")
+    return {"us": us, "TFLOPs": tfs, "steps": steps}
+
+
+def cpu_baseline(cases, max_seconds=20.0):
+    """Time the oracle's C restatement of the reference CPU path on the host (bounded sample)."""
+    import numpy as np
+    from oracle import c_oracle, quant
+    nthreads = max(1, min(16, os.cpu_count() or 1))
+    total_b, total_t, done = 0, 0.0, []
+    t_start = time.perf_counter()
+    for name, N, K, M in cases:
+        q, scales = quant.gen_codes_scales(N, K, G, 7)
+        Wp = quant.pack_int4(q)
+        x = np.random.default_rng(8).standard_normal((M, K)).astype(np.float16)
+        c_oracle.forward(Wp, x, scales, N, K, G, nthreads)          # warm-up
+        t0 = time.perf_counter()
+        c_oracle.forward(Wp, x, scales, N, K, G, nthreads)
+        dt = time.perf_counter() - t0
+        total_b += alg_bytes(M, N, K)
+        total_t += dt
+        done.append(f"{name} M={M}")
+        if time.perf_counter() - t_start > max_seconds:
+            break
+    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "sample": f"oracle C path (unpack + fp16 dequant + fp32 GEMM), one timed call each of: {', '.join(done)}; "
+                      f"{total_t:.2f} s timed, {nthreads} OpenMP threads, host {os.cpu_count()} cpus"}
+
+
+def cpu_baseline_prefill(max_seconds=15.0):
+    """Prefill CPU reference rate on a bounded N-slice of config 4 (rate is size-independent)."""
+    import numpy as np
+    from oracle import c_oracle, quant
+    nthreads = max(1, min(16, os.cpu_count() or 1))
+    _, N, K, M = PREFILL_CASE
+    Ns = 1024
+    q, scales = quant.gen_codes_scales(Ns, K, G, 9)
+    Wp = quant.pack_int4(q)
+    x = np.random.default_rng(10).standard_normal((M, K)).astype(np.float16)
+    t0 = time.perf_counter()
+    c_oracle.forward(Wp, x, scales, Ns, K, G, nthreads)
+    dt = time.perf_counter() - t0
+    return {"value": round(alg_flops(M, Ns, K) / dt / 1e12, 4), "unit": "TFLOP/s", "cores": nthreads,
+            "kind": "port", "sample": f"oracle C path on an N={Ns} column slice of M=2048, K=8192 ({dt:.2f} s)"}
+
+
+def load_traffic(kind):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kind)
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
+    ap.add_argument("--json", default=None, help="also write the JSON line to this file")
+    a = ap.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the op is single-GPU; see DESIGN.md for how "
+              "it would shard); use --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU available", file=sys.stderr)
+        return 2
+    from w4a16_opt import w4a16_gemm as gemm          # in-tree HIP build; no fallback
+    torch.manual_seed(0)
+    dev = torch.cuda.get_device_properties(0)
+    log(f"device: {dev.name} ({getattr(dev, 'gcnArchName', '?')}), CUs={dev.multi_processor_count}")
+
+    dec = pre = None
+    if a.workload == "decode" or not a.no_prefill:
+        pass
+    dec = bench_decode(torch, gemm, a.steps, a.warmup) if a.workload == "decode" else None
+    if a.workload == "prefill" or not a.no_prefill:
+        pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
+                            a.warmup if a.workload == "prefill" else 3)
+
+    out = {"metric": "decode GB/s & %HBM peak (M=1..16); prefill TFLOP/s & %MFMA peak (M=2048)"}
+    if dec is not None:
+        ach = dec["bytes_per_launch"] / (dec["avg_launch_us"] * 1e-6) / 1e9
+        out.update({
+            "value": round(dec["value"], 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+            "ms_per_step": round(dec["ms_per_step"], 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
+            "config": {"workload": "BASELINE configs[1]: decode, Llama-3-8B MLP gate/up K=4096 N=14336 and down "
+                                   "K=14336 N=4096, M in {1,4,8,16}, G=128; one step = the 8 calls",
+                       "G": G, "weight_copies_per_shape": dec["copies"], "timing": "HIP graph replay, HIP events"},
+            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": load_traffic("decode"),
+                         "kernel": "w4a16::decode_kernel", "bytes_per_launch": dec["bytes_per_launch"],
+                         "avg_launch_us": round(dec["avg_launch_us"], 3)},
+            "cases": dec["cases"],
+        })
+    if pre is not None:
+        _, N, K, M = PREFILL_CASE
+        pre_obj = {"value": round(pre["TFLOPs"], 1), "unit": "TFLOP/s", "us_per_call": round(pre["us"], 1),
+                   "config": {"workload": "BASELINE configs[3]: prefill M=2048 K=8192 N=28672 G=128"},
+                   "roofline": {"bound": "mfma", "achieved": round(pre["TFLOPs"], 1), "peak": FP16_MFMA_PEAK_TFS,
+                                "unit": "TFLOP/s", "frac": round(pre["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
+                                "traffic": load_traffic("prefill"), "kernel": "w4a16::prefill_kernel",
+                                "flops_per_launch": alg_flops(M, N, K)}}
+        if dec is None:
+            out.update({"value": pre_obj["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps,
+                        "warmup": a.warmup, "ms_per_step": round(pre["us"] / 1e3, 5), "higher_is_better": True,
+                        "scaling": "weak", "vs_baseline": None, "dtype": "fp16 (fp32 accumulate)",
+                        "data": "synthetic", "config": pre_obj["config"], "roofline": pre_obj["roofline"]})
+        else:
+            out["prefill"] = pre_obj
+    if not a.no_cpu:
+        if dec is not None:
+            out["cpu_baseline"] = cpu_baseline(DECODE_CASES)
+            if pre is not None:
+                out["prefill"]["cpu_baseline"] = cpu_baseline_prefill()
+        else:
+            out["cpu_baseline"] = cpu_baseline_prefill()
+    line = json.dumps(out)
+    print(line, flush=True)
+    if a.json:
+        with open(a.json, "w") as f:
+            f.write(line + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

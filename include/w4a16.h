@@ -68,13 +68,13 @@ typedef struct w4a16_device_limits {
 typedef struct w4a16_plan {
     int32_t M, N, K, G;
     int32_t kernel;           /* 0 = decode, 1..4 = prefill tile config                 */
-    int32_t splits;           /* decode: number of K slabs reduced across workgroups     */
-    int32_t slab_chunks;      /* decode: 64-wide K chunks per slab                       */
+    int32_t splits;           /* decode: number of K ranges reduced across workgroups    */
+    int32_t slab_chunks;      /* decode: 64-wide K chunks per wave                       */
     int32_t tile_n;           /* decode: output columns per workgroup                    */
     int32_t grid;             /* workgroups launched by the main kernel                  */
     int32_t block;            /* threads per workgroup                                   */
     int32_t counter_slots;    /* ints of the counter buffer used (decode split-K fixup)  */
-    int32_t reserved;
+    int32_t decode_variant;   /* decode: kernel shape id (waves, n16 blocks per wave)     */
     uint64_t workspace_bytes; /* bytes of fp32 partials the launch needs (0 if none)     */
 } w4a16_plan;
 

@@ -1,0 +1,186 @@
+"""CPU tests of the C ABI (include/w4a16.h) of libw4a16_hip.so: exports, validation, routing,
+planning.  Only pure host entry points are called (no device work), so these run without a GPU.
+
+The validation order and messages mirror the reference op (src/vectorized/kernel.cu:219-249) and
+the substrings its tests match (tests/test_w4a16.py:188-195, 281-305).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "w4a16-gemm_amd", "libw4a16_hip.so")
+HEADER = os.path.join(ROOT, "include", "w4a16.h")
+
+
+class Problem(ctypes.Structure):
+    _fields_ = [("M", ctypes.c_int64), ("K", ctypes.c_int64), ("N", ctypes.c_int64),
+                ("groups", ctypes.c_int64), ("wp_words", ctypes.c_int64),
+                ("Wp", ctypes.c_void_p), ("x", ctypes.c_void_p), ("scales", ctypes.c_void_p)]
+
+
+class Limits(ctypes.Structure):
+    _fields_ = [("cu_count", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32),
+                ("max_threads_per_block", ctypes.c_int32), ("gcn_arch", ctypes.c_int32)]
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("M", "N", "K", "G", "kernel", "splits", "slab_chunks", "tile_n",
+                                              "grid", "block", "counter_slots", "decode_variant")] + \
+               [("workspace_bytes", ctypes.c_uint64)]
+
+
+MI355X = Limits(256, 160 * 1024, 1024, 950)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} not built (python w4a16-gemm_amd/build.py)")
+    L = ctypes.CDLL(LIB)
+    L.w4a16_plan_create.argtypes = [ctypes.POINTER(Problem), ctypes.c_int, ctypes.POINTER(Limits),
+                                    ctypes.POINTER(Plan), ctypes.c_char_p, ctypes.c_size_t]
+    L.w4a16_plan_create.restype = ctypes.c_int
+    L.w4a16_max_counter_slots.restype = ctypes.c_int32
+    L.w4a16_last_error.restype = ctypes.c_char_p
+    return L
+
+
+def plan(lib, M, N, K, G=None, variant=-1, groups=None, wp_words=None, ptrs=(0, 0, 0), limits=MI355X):
+    if groups is None:
+        groups = K // G if G else 1
+    if wp_words is None:
+        wp_words = N * K // 8
+    p = Problem(M, K, N, groups, wp_words, *ptrs)
+    out = Plan()
+    err = ctypes.create_string_buffer(512)
+    rc = lib.w4a16_plan_create(ctypes.byref(p), variant, ctypes.byref(limits), ctypes.byref(out), err, 512)
+    return rc, out, err.value.decode()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    text = open(HEADER).read()
+    names = re.findall(r"^\s*(?:int|int32_t|const char\*|void)\s+(w4a16_\w+)\s*\(", text, re.M)
+    assert len(names) >= 6, names
+    for n in names:
+        assert hasattr(lib, n), f"libw4a16_hip.so does not export {n}"
+    assert lib.w4a16_abi_version() == 1
+
+
+def test_plan_struct_layout_matches_header(lib):
+    text = open(HEADER).read()
+    body = text[text.index("typedef struct w4a16_plan"):text.index("} w4a16_plan;")]
+    fields = re.findall(r"(?:int32_t|uint64_t)\s+([\w, ]+);", body)
+    flat = [f.strip() for grp in fields for f in grp.split(",")]
+    assert flat == [f[0] for f in Plan._fields_]
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(M=2, N=64, K=512, G=64, variant=7), "variant"),
+    (dict(M=2, N=64, K=512, G=64, variant=-2), "variant"),
+    (dict(M=0, N=64, K=512, G=64), "M must be at least 1"),
+    (dict(M=1 << 31, N=64, K=512, G=64), "dimensions must fit in int32"),
+    (dict(M=2, N=64, K=32, G=32), "multiple of 64"),
+    (dict(M=2, N=24, K=512, G=64), "multiple of 16"),
+    (dict(M=2, N=64, K=512, groups=3), "divisible by the number of groups"),
+    (dict(M=2, N=64, K=512, groups=0), "divisible by the number of groups"),
+    (dict(M=2, N=64, K=512, G=64, wp_words=10), "N\\*K/8"),
+    (dict(M=2, N=64, K=512, G=64, ptrs=(16, 8, 16)), "16-byte aligned"),
+    (dict(M=2, N=64, K=512, G=32), "unsupported group size 32"),
+    (dict(M=2, N=64, K=512, G=256), "unsupported group size 256"),
+    (dict(M=32, N=64, K=512, G=64, variant=0), "decode kernel needs"),
+    (dict(M=4, N=80, K=640, G=64, variant=0), "decode kernel needs"),
+    (dict(M=4, N=64, K=576, G=64, variant=0), "decode kernel needs"),
+])
+def test_validation_messages(lib, kw, msg):
+    rc, _, err = plan(lib, **kw)
+    assert rc == 1, (kw, rc, err)
+    assert re.search(msg, err), (kw, err)
+
+
+def test_validation_order_follows_reference(lib):
+    """kernel.cu checks variant, M, int32, K%64, N%16, groups, numel, alignment, G in this order."""
+    assert "variant" in plan(lib, M=0, N=24, K=32, G=32, variant=9)[2]
+    assert "M must" in plan(lib, M=0, N=24, K=32, G=32)[2]
+    assert "multiple of 64" in plan(lib, M=1, N=24, K=32, G=32)[2]
+    assert "multiple of 16" in plan(lib, M=1, N=24, K=512, G=32)[2]
+    assert "groups" in plan(lib, M=1, N=32, K=512, groups=3, wp_words=1)[2]
+    assert "N*K/8" in plan(lib, M=1, N=32, K=512, G=32, wp_words=1, ptrs=(1, 1, 1))[2]
+    assert "aligned" in plan(lib, M=1, N=32, K=512, G=32, ptrs=(1, 1, 1))[2]
+    assert "group size" in plan(lib, M=1, N=32, K=512, G=32)[2]
+
+
+@pytest.mark.parametrize("M,N,K,kernel", [
+    (1, 4096, 4096, 0), (16, 14336, 4096, 0), (16, 4096, 14336, 0),       # decode contract
+    (17, 4096, 4096, None), (1, 4112, 4160, None), (4, 80, 640, None),     # prefill
+    (3, 48, 192, None), (128, 14336, 4096, None), (2048, 28672, 8192, None),
+])
+def test_routing(lib, M, N, K, kernel):
+    rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
+    assert rc == 0, err
+    if kernel == 0:
+        assert p.kernel == 0
+    else:
+        assert 1 <= p.kernel <= 4
+
+
+@pytest.mark.parametrize("v", [1, 2, 3, 4])
+def test_forced_prefill_variant_is_used(lib, v):
+    rc, p, err = plan(lib, M=3, N=64, K=512, G=64, variant=v)
+    assert rc == 0 and p.kernel == v
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
+@pytest.mark.parametrize("N,K", [(64, 512), (4096, 4096), (14336, 4096), (4096, 14336), (28672, 4096),
+                                 (6144, 4096), (1024, 2048), (512, 4096), (4096, 11264)])
+def test_decode_plan_invariants(lib, M, N, K):
+    rc, p, err = plan(lib, M=M, N=N, K=K, G=128)
+    assert rc == 0 and p.kernel == 0, err
+    KC = K // 64
+    waves = p.block // 64
+    assert p.splits * waves * p.slab_chunks == KC
+    assert N % p.tile_n == 0 and p.grid == (N // p.tile_n) * p.splits
+    assert 0 < p.block <= 1024
+    if p.splits > 1:
+        assert p.workspace_bytes == p.splits * M * N * 4
+        assert p.counter_slots == N // p.tile_n <= lib.w4a16_max_counter_slots()
+    else:
+        assert p.workspace_bytes == 0 and p.counter_slots == 0
+
+
+@pytest.mark.parametrize("M", [1, 17, 100, 513, 2048, 70000])
+@pytest.mark.parametrize("N", [16, 4112, 28672])
+def test_prefill_plan_invariants(lib, M, N):
+    rc, p, err = plan(lib, M=M, N=N, K=4160, G=64)
+    assert rc == 0, err
+    tiles = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128)}[p.kernel]
+    assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
+    assert p.workspace_bytes == 0 and p.counter_slots == 0
+
+
+def test_empty_n_plans_nothing(lib):
+    rc, p, err = plan(lib, M=4, N=0, K=512, G=64)
+    assert rc == 0
+
+
+def test_injected_small_lds_limit_reports_no_config(lib):
+    tiny = Limits(256, 1024, 1024, 950)
+    rc, _, err = plan(lib, M=1, N=4096, K=4096, G=128, limits=tiny)
+    assert rc == 2 and "no pipeline configuration fits in 1024 B of shared memory" in err
+    rc, _, err = plan(lib, M=300, N=4096, K=4096, G=128, limits=tiny)
+    assert rc == 2 and "no prefill configuration fits" in err
+    rc, _, err = plan(lib, M=300, N=4096, K=4096, G=128, variant=4, limits=Limits(256, 30000, 1024, 950))
+    assert rc == 2 and "no prefill configuration fits" in err
+
+
+def test_torch_binding_imports_and_rejects_host_tensors():
+    """The extension module loads on CPU and rejects non-device tensors first (kernel.cu:219)."""
+    torch = pytest.importorskip("torch")
+    import w4a16_opt
+    with pytest.raises(RuntimeError, match="CUDA"):
+        w4a16_opt.w4a16_gemm(torch.zeros(8, dtype=torch.int32), torch.zeros(1, 64, dtype=torch.half),
+                             torch.zeros(1, 16, dtype=torch.half))

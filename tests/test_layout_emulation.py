@@ -1,0 +1,207 @@
+"""numpy emulation of the MI355X kernels' index math against a plain float64 matmul (CPU).
+
+The same method as the reference's tests/layout_prefill.py (which emulates its NVIDIA fragment
+layouts), applied to this build's gfx950 mapping (w4a16-gemm_amd/csrc/w4a16_device.h):
+  * v_mfma_f32_16x16x32_f16 modelled as C[i][j] += sum over (lane group kb, slot) of
+    A[16*kb + i][slot] * B[16*kb + j][slot]; output lane l holds C[4*(l//16) + r][l % 16];
+  * A operand: lane (kb, i) reads packed lane' = 4*(i % 8) + kb, keeps its own nibble parity,
+    MFMA h uses words 2h, 2h+1 (slot pair c <-> k = 32h + 8c + 2kb + {0,1});
+  * B operand, prefill: the permuted LDS row layout written by lds_store_xseg and read with
+    one 16-byte read at row*144 + h*64 + kb*16;
+  * B operand, decode: 8 consecutive halves per lane then the 4x4 cross-row transpose made of
+    v_permlane32_swap (upper half of dst <-> lower half of src) and v_permlane16_swap (odd
+    rows of dst <-> even rows of src);
+  * decode: waves split K, partial tiles summed in wave order, splits summed in split order.
+Exact float64 arithmetic is used (dequantised values are exact), so the check is 1e-12.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import quant
+
+XROW = 144
+
+
+def permlane32_swap(dst, src):
+    """v_permlane32_swap_b32: lanes 32..63 of dst <-> lanes 0..31 of src."""
+    d, s = dst.copy(), src.copy()
+    d[32:], s[:32] = src[:32].copy(), dst[32:].copy()
+    return d, s
+
+
+def permlane16_swap(dst, src):
+    """v_permlane16_swap_b32: rows 1 and 3 of dst <-> rows 0 and 2 of src."""
+    d, s = dst.copy(), src.copy()
+    for r in (0, 2):
+        d[16 * (r + 1):16 * (r + 2)], s[16 * r:16 * (r + 1)] = src[16 * r:16 * (r + 1)].copy(), dst[16 * (r + 1):16 * (r + 2)].copy()
+    return d, s
+
+
+def xpose_rows(v):
+    """w4a16::xpose_rows on a [64 lanes, 4 dwords] array (dwords as opaque objects)."""
+    a0, a1 = permlane32_swap(v[:, 0], v[:, 2])
+    b0, b1 = permlane32_swap(v[:, 1], v[:, 3])
+    c0, c1 = permlane16_swap(a0, b0)
+    e0, e1 = permlane16_swap(a1, b1)
+    return np.stack([c0, c1, e0, e1], axis=1)
+
+
+def mfma(A, B, C):
+    """A, B: [64 lanes, 8 slots]; C: [64 lanes, 4] in the 16x16 output layout."""
+    Am = np.zeros((16, 16))
+    out = C.copy()
+    full = np.zeros((16, 16))
+    for kb in range(4):
+        full += A[16 * kb:16 * kb + 16, :] @ B[16 * kb:16 * kb + 16, :].T
+    for lane in range(64):
+        for r in range(4):
+            out[lane, r] += full[4 * (lane // 16) + r, lane % 16]
+    del Am
+    return out
+
+
+def a_operand(W4, Sn, nb, kc, h):
+    """Dequantised A operand of one MFMA: lane (kb, i) -> 8 fp64 values.  W4: [NB,KC,32,4] uint32,
+    Sn: per-(nb, kc) scale row [16] for n = 16nb + i."""
+    A = np.zeros((64, 8))
+    for lane in range(64):
+        kb, i = lane >> 4, lane & 15
+        lanep = 4 * (i & 7) + kb
+        pe = i >> 3
+        s = Sn[i]
+        slots = []
+        for word in (2 * h, 2 * h + 1):
+            w = int(W4[nb, kc, lanep, word])
+            for sh in (0, 8):                       # pairs p = pe (sh 0) and p = pe + 2 (sh 8)
+                bits = (w >> (sh + 4 * pe)) & 0x000F000F
+                slots += [((bits & 0xF) - 8) * s, ((bits >> 16) - 8) * s]
+        A[lane] = slots
+    return A
+
+
+@pytest.mark.parametrize("M,N,K,G,BM,BN,WMs,WNs", [
+    (5, 48, 192, 64, 16, 128, 1, 4), (17, 80, 256, 64, 32, 128, 1, 4),
+    (33, 144, 640, 128, 64, 128, 2, 2), (70, 208, 384, 64, 128, 128, 2, 2),
+])
+def test_prefill_index_math(M, N, K, G, BM, BN, WMs, WNs):
+    rng = np.random.default_rng(M + N)
+    q = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    s = rng.random((K // G, N)) * 0.05 + 0.001
+    x = rng.standard_normal((M, K))
+    W4 = quant.pack_int4(q).view(np.uint32).reshape(N // 16, K // 64, 32, 4)
+    ref = x @ ((q.astype(np.float64) - 8) * np.repeat(s.T, G, axis=1)).T
+    WM, WN = BM // WMs, BN // WNs
+    TM, TN = WM // 16, WN // 16
+    KC, NBLK = K // 64, N // 16
+    y = np.full((M, N), np.nan)
+    for tm in range(-(-M // BM)):
+        for tn in range(-(-N // BN)):
+            m0, n0 = tm * BM, tn * BN
+            accs = {}
+            for kc in range(KC):
+                # x chunk -> permuted LDS (one float64 per half; index = byte offset / 2)
+                lds = np.zeros(BM * XROW // 2)
+                for row in range(BM):
+                    for qseg in range(8):
+                        v = x[m0 + row, kc * 64 + 8 * qseg: kc * 64 + 8 * qseg + 8] if m0 + row < M else np.zeros(8)
+                        base = row * XROW + (qseg >> 2) * 64 + (qseg & 3) * 4
+                        for e in range(4):
+                            lds[(base + 16 * e) // 2:(base + 16 * e) // 2 + 2] = v[2 * e:2 * e + 2]
+                for wave in range(WMs * WNs):
+                    wm, wn = wave // WNs, wave % WNs
+                    for b in range(TN):
+                        nb = (n0 >> 4) + wn * TN + b
+                        if nb >= NBLK:
+                            continue
+                        Sn = s[kc * 64 // G, nb * 16:nb * 16 + 16]
+                        for h in range(2):
+                            A = a_operand(W4, Sn, nb, kc, h)
+                            for t in range(TM):
+                                B = np.zeros((64, 8))
+                                for lane in range(64):
+                                    kb, li = lane >> 4, lane & 15
+                                    off = ((wm * WM + t * 16 + li) * XROW + h * 64 + kb * 16) // 2
+                                    B[lane] = lds[off:off + 8]
+                                key = (wave, t, b)
+                                accs[key] = mfma(A, B, accs.get(key, np.zeros((64, 4))))
+            for (wave, t, b), C in accs.items():
+                wm, wn = wave // WNs, wave % WNs
+                nb = (n0 >> 4) + wn * TN + b
+                for lane in range(64):
+                    m = m0 + wm * WM + t * 16 + (lane & 15)
+                    if m < M:
+                        n = nb * 16 + 4 * (lane >> 4)
+                        y[m, n:n + 4] = C[lane]
+    assert not np.isnan(y).any()
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-12
+
+
+def test_xpose_rows_is_the_b_operand_transpose():
+    """Lane (row r) holding dwords D[r][0..3] ends with D[0..3][r] (w4a16_device.h mapping)."""
+    D = np.array([[(r, e) for e in range(4)] for r in range(4)], dtype=object)
+    v = np.empty((64, 4), dtype=object)
+    for lane in range(64):
+        for e in range(4):
+            v[lane, e] = (lane >> 4, e, lane & 15)
+    out = xpose_rows(v)
+    for lane in range(64):
+        r = lane >> 4
+        assert [tuple(out[lane, c]) for c in range(4)] == [(c, r, lane & 15) for c in range(4)]
+    del D
+
+
+@pytest.mark.parametrize("M,N,K,G,NBW,WAVES,splits", [
+    (1, 64, 512, 64, 1, 8, 1), (3, 128, 1024, 128, 2, 8, 2), (16, 64, 1024, 64, 4, 4, 2),
+])
+def test_decode_index_math(M, N, K, G, NBW, WAVES, splits):
+    rng = np.random.default_rng(M * 7 + N)
+    q = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    s = rng.random((K // G, N)) * 0.05 + 0.001
+    x = rng.standard_normal((M, K))
+    W4 = quant.pack_int4(q).view(np.uint32).reshape(N // 16, K // 64, 32, 4)
+    ref = x @ ((q.astype(np.float64) - 8) * np.repeat(s.T, G, axis=1)).T
+    KC = K // 64
+    kcw = KC // (splits * WAVES)
+    y = np.full((M, N), np.nan)
+    for tile in range(N // (16 * NBW)):
+        parts = []
+        for split in range(splits):
+            red = np.zeros((WAVES, NBW, 64, 4))
+            for wave in range(WAVES):
+                kc0 = (split * WAVES + wave) * kcw
+                for c in range(kcw):
+                    kc = kc0 + c
+                    Bs = []
+                    for h in range(2):
+                        v = np.empty((64, 4), dtype=object)
+                        for lane in range(64):
+                            kb, li = lane >> 4, lane & 15
+                            row = min(li, M - 1)
+                            base = kc * 64 + 32 * h + 8 * kb
+                            for e in range(4):
+                                v[lane, e] = (x[row, base + 2 * e], x[row, base + 2 * e + 1])
+                        t = xpose_rows(v)
+                        Bs.append(np.array([[val for dw in t[lane] for val in dw] for lane in range(64)]))
+                    for b in range(NBW):
+                        nb = tile * NBW + b
+                        Sn = s[kc * 64 // G, nb * 16:nb * 16 + 16]
+                        for h in range(2):
+                            red[wave, b] = mfma(a_operand(W4, Sn, nb, kc, h), Bs[h], red[wave, b])
+            tot = red[0].copy()
+            for w in range(1, WAVES):
+                tot += red[w]
+            parts.append(tot)
+        fin = parts[0].copy()
+        for p in parts[1:]:
+            fin += p
+        for b in range(NBW):
+            nb = tile * NBW + b
+            for lane in range(64):
+                li = lane & 15
+                if li < M:
+                    n = nb * 16 + 4 * (lane >> 4)
+                    y[li, n:n + 4] = fin[b, lane]
+    assert not np.isnan(y).any()
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-12

@@ -25,10 +25,23 @@ constexpr int kLdsRowBytes = 144;
 constexpr int prefill_lds_bytes(int cfg) { return 2 * kPrefillTable[cfg].bm * kLdsRowBytes; }
 constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n; }
 
-// Decode: 4 waves per workgroup, one n16 block each -> 64 output channels per workgroup.
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeTileN = 16 * kDecodeWaves;
-constexpr int decode_lds_bytes(int ks) { return 16 * (ks * 128 + 16) + 16; }
+// Decode kernel shapes: NBW n16 blocks (16*NBW output channels) per workgroup, WAVES waves
+// splitting the workgroup's K range, software-pipeline depth D (chunks in flight per wave).
+struct DecodeCfg {
+    int nbw, waves, depth;
+};
+constexpr DecodeCfg kDecodeTable[8] = {
+    {1, 16, 4},   // 0
+    {1, 16, 2},   // 1
+    {2, 16, 4},   // 2
+    {2, 16, 2},   // 3
+    {1, 8, 4},    // 4
+    {2, 8, 4},    // 5
+    {4, 8, 4},    // 6
+    {4, 16, 2},   // 7
+};
+constexpr int kNumDecodeCfg = 8;
+constexpr int decode_lds_bytes(int v) { return kDecodeTable[v].waves * kDecodeTable[v].nbw * 64 * 16 + 16; }
 
 // Counter buffer size (ints) the library may ask for: one per decode column tile.
 constexpr int32_t kMaxCounterSlots = 1 << 18;

@@ -19,26 +19,38 @@ namespace w4a16 {
 // ------------------------------------------------------------------------------------ decode
 // Replaces the reference decode kernel w4a16_gemm_mma (src/vectorized/decode.cuh:18-159).
 //
-// Grid: (N / (16*WAVES)) column tiles x `splits` K slabs, one workgroup each (slab index is the
-// fastest-varying part of blockIdx.x).  Wave w of a workgroup owns n16 block
-// tile*WAVES + w over KS 64-wide chunks.  All KS weight word-quads of the wave are issued up
-// front (16 B per lane each) so the whole slab is in flight at once; the slab of x (M rows) is
-// staged once into LDS in the permuted B-operand layout and shared by the WAVES waves.
+// Workgroup = WAVES waves on one column tile of NBW n16 blocks (16*NBW output channels); the
+// waves split the workgroup's K range, wave w taking `kcw` consecutive 64-wide chunks.  Each
+// wave streams its weight word quads and its x fragments straight from memory into VGPRs
+// (software pipeline of depth D chunks), dequantises in registers and accumulates with MFMA.
+// The x fragment of a chunk half is one 16-byte load of 8 consecutive halves per lane followed
+// by a 4x4 transpose across the four 16-lane rows (v_permlane32_swap + v_permlane16_swap),
+// which yields the B operand layout of w4a16_device.h without LDS.  Token rows >= M load row
+// M-1; such columns of the MFMA only feed outputs that are never stored.
 //
-// Each wave accumulates its 16 (n) x 16 (token) tile in fp32 over the slab in K order.  With
-// splits > 1 the fp32 partial goes to workspace[split][m][n]; the last workgroup of a column
-// tile to finish (device-scope counter) adds the partials in split order 0..splits-1 and
-// writes fp16 y, then resets its counter to zero.  The summation order is therefore fixed and
-// the result is deterministic run to run (reference test_deterministic, test_w4a16.py:258-261).
-template <int WAVES, int KS>
+// The WAVES partial tiles are summed through LDS in wave order.  When the K range is split
+// over `splits` workgroups (grid = column tiles x splits, split fastest), each workgroup's fp32
+// tile goes to workspace[split][m][n] and the last workgroup of the column tile to arrive
+// (device-scope counter) adds the partials in split order and writes fp16 y.  Every sum is in a
+// fixed order, so results are deterministic (reference test_deterministic, test_w4a16.py:258).
+
+// 4x4 transpose of dwords across the four 16-lane rows: lane (row r, p) holds v[e] = D[r][e]
+// on entry and D[e][r] on exit.
+__device__ __forceinline__ u4 xpose_rows(u4 v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto e = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    return u4{c[0], c[1], e[0], e[1]};
+}
+
+template <int NBW, int WAVES, int D>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
               const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
               float* __restrict__ ws, int* __restrict__ counters,
-              int M, int N, int K, int gshift, int splits) {
-    constexpr int NT = WAVES * 64;
-    constexpr int XROWB = KS * 128 + 16;            // LDS bytes per token row of the slab
-    __shared__ __attribute__((aligned(16))) char xs[16 * XROWB];
+              int M, int N, int K, int gshift, int splits, int kcw) {
+    __shared__ __attribute__((aligned(16))) f4 red[WAVES][NBW][64];
     __shared__ int s_last;
 
     const int tid = threadIdx.x;
@@ -49,75 +61,123 @@ decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int split = blockIdx.x % splits;
     const int tile = blockIdx.x / splits;
     const int KC = K >> 6;
-    const int kc0 = split * KS;
-    const int nb = tile * WAVES + wave;
+    const int kc0 = (split * WAVES + wave) * kcw;           // this wave's first chunk
+    const int nb0 = tile * NBW;
     const int lanep = ((li & 7) << 2) | kb;
 
-    // 1. the wave's weight slab: KS word quads per lane, all in flight together.
-    const u4* wsrc = Wp + ((size_t)nb * KC + kc0) * 32 + lanep;
-    u4 wv[KS];
+    const u4* wsrc[NBW];
+    const uint16_t* ssrc[NBW];
 #pragma unroll
-    for (int c = 0; c < KS; ++c) wv[c] = __builtin_nontemporal_load(wsrc + (size_t)c * 32);
-    const uint16_t* ssrc = scales + (size_t)nb * 16 + li;
-    uint16_t sv[KS];
-#pragma unroll
-    for (int c = 0; c < KS; ++c) sv[c] = ssrc[(size_t)((kc0 + c) >> gshift) * N];
-
-    // 2. x slab -> LDS (only the M real token rows are stored).
-    const int segs = M * KS * 8;
-    for (int sg = tid; sg < segs; sg += NT) {
-        const int m = sg / (KS * 8);
-        const int rem = sg - m * (KS * 8);
-        const int c = rem >> 3;
-        const int q = rem & 7;
-        const u4 v = *reinterpret_cast<const u4*>(x + (size_t)m * K + (size_t)(kc0 + c) * 64 + q * 8);
-        lds_store_xseg(xs + m * XROWB + c * 128, q, v);
+    for (int b = 0; b < NBW; ++b) {
+        wsrc[b] = Wp + ((size_t)(nb0 + b) * KC + kc0) * 32 + lanep;
+        ssrc[b] = scales + (size_t)(nb0 + b) * 16 + li;
     }
-    __syncthreads();
+    const uint16_t* xsrc = x + (size_t)min(li, M - 1) * K + (size_t)kc0 * 64 + kb * 8;
 
-    // 3. dequantise + MFMA over the slab in K order.
+    u4 wq[D][NBW];
+    u4 xq[D][2];
+    uint16_t sq[D][NBW];
+    auto issue = [&](int c, int slot) {
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) wq[slot][b] = __builtin_nontemporal_load(wsrc[b] + (size_t)c * 32);
+        xq[slot][0] = *reinterpret_cast<const u4*>(xsrc + (size_t)c * 64);
+        xq[slot][1] = *reinterpret_cast<const u4*>(xsrc + (size_t)c * 64 + 32);
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) sq[slot][b] = ssrc[b][(size_t)((kc0 + c) >> gshift) * N];
+    };
+
     const Dq d = dq_setup(lane);
-    const bool tok_ok = li < M;
-    const char* xb = xs + li * XROWB + kb * 16;
-    const h8 zero8 = {};
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    f4 acc[NBW];
 #pragma unroll
-    for (int c = 0; c < KS; ++c) {
-        const h2 s2 = scale2(sv[c]);
-        const h8 a0 = dq_frag(wv[c].x, wv[c].y, d, s2);
-        const h8 a1 = dq_frag(wv[c].z, wv[c].w, d, s2);
-        const h8 b0 = tok_ok ? *reinterpret_cast<const h8*>(xb + c * 128) : zero8;
-        const h8 b1 = tok_ok ? *reinterpret_cast<const h8*>(xb + c * 128 + 64) : zero8;
-        acc = mfma16x16x32(a0, b0, acc);
-        acc = mfma16x16x32(a1, b1, acc);
+    for (int b = 0; b < NBW; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+        if (i < kcw) issue(i, i);
+    for (int c0 = 0; c0 < kcw; c0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            if (c0 + i >= kcw) break;
+            const h8 b0 = __builtin_bit_cast(h8, xpose_rows(xq[i][0]));
+            const h8 b1 = __builtin_bit_cast(h8, xpose_rows(xq[i][1]));
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) {
+                const h2 s2 = scale2(sq[i][b]);
+                const h8 a0 = dq_frag(wq[i][b].x, wq[i][b].y, d, s2);
+                const h8 a1 = dq_frag(wq[i][b].z, wq[i][b].w, d, s2);
+                acc[b] = mfma16x16x32(a0, b0, acc[b]);
+                acc[b] = mfma16x16x32(a1, b1, acc[b]);
+            }
+            if (c0 + D + i < kcw) issue(c0 + D + i, i);
+        }
     }
 
-    // lane holds token li, channels n .. n+3
-    const int n = nb * 16 + 4 * kb;
+    // Cross-wave reduction in wave order.
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) red[wave][b][lane] = acc[b];
+    __syncthreads();
+    f4 sum = {0.f, 0.f, 0.f, 0.f};
+    const int rb = tid >> 6;                                // n16 block this thread finishes
+    if (tid < NBW * 64) {
+        sum = red[0][rb][lane];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) sum += red[w][rb][lane];
+    }
+    // thread (rb, lane) now holds token li, channels n .. n+3 of the workgroup's tile
+    const int n = (nb0 + rb) * 16 + 4 * kb;
+    const bool mine = tid < NBW * 64 && li < M;
     if (splits == 1) {
-        if (tok_ok) *reinterpret_cast<u2*>(y + (size_t)li * N + n) = pack_f16x4(acc);
+        if (mine) *reinterpret_cast<u2*>(y + (size_t)li * N + n) = pack_f16x4(sum);
         return;
     }
-    if (tok_ok) *reinterpret_cast<f4*>(ws + ((size_t)split * M + li) * N + n) = acc;
-    __threadfence();                                  // release the partial (agent scope)
+    // Split-K hand-off without agent-scope fences (those write back / invalidate the XCD's whole
+    // L2): the partials travel through agent-scope atomic stores/loads, which are coherent at
+    // device scope by themselves, and every wave waits for its stores to complete
+    // (s_waitcnt vmcnt(0)) before the workgroup's counter RMW.
+    if (mine) {
+        unsigned long long* p = reinterpret_cast<unsigned long long*>(ws + ((size_t)split * M + li) * N + n);
+        const u4 bits = __builtin_bit_cast(u4, sum);
+        __hip_atomic_store(p, (unsigned long long)bits.x | ((unsigned long long)bits.y << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 1, (unsigned long long)bits.z | ((unsigned long long)bits.w << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&counters[tile], 1) == splits - 1);
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&counters[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
     if (!s_last) return;
-    __threadfence();                                  // acquire the other slabs' partials
 
-    constexpr int TW4 = WAVES * 4;                    // float4 columns per tile
-    const int n0 = tile * WAVES * 16;
-    const size_t sstride = (size_t)M * N;
-    for (int e = tid; e < M * TW4; e += NT) {
-        const int m = e / TW4;
-        const int c4 = e - m * TW4;
-        const float* p = ws + (size_t)m * N + n0 + c4 * 4;
-        f4 sum = *reinterpret_cast<const f4*>(p);
-        for (int s = 1; s < splits; ++s) sum += *reinterpret_cast<const f4*>(p + (size_t)s * sstride);
-        *reinterpret_cast<u2*>(y + (size_t)m * N + n0 + c4 * 4) = pack_f16x4(sum);
+    // Last arrival: thread (m, c4) adds the `splits` partials of its 4 channels in split order,
+    // issuing the loads of up to 8 splits at once.
+    constexpr int C4 = NBW * 4;                              // float4 groups per row of the tile
+    if (tid < M * C4) {
+        const int m = tid / C4;
+        const int c4 = tid - m * C4;
+        const int nn = nb0 * 16 + c4 * 4;
+        const unsigned long long* p = reinterpret_cast<const unsigned long long*>(ws + (size_t)m * N + nn);
+        const size_t sstride = (size_t)M * N / 2;           // in 8-byte words
+        f4 tot = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < splits; s0 += 8) {
+            unsigned long long lo[8], hi[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (s0 + j < splits) {
+                    lo[j] = __hip_atomic_load(p + (size_t)(s0 + j) * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    hi[j] = __hip_atomic_load(p + (size_t)(s0 + j) * sstride + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (s0 + j < splits) {
+                    const f4 v = __builtin_bit_cast(f4, u4{(uint32_t)lo[j], (uint32_t)(lo[j] >> 32),
+                                                           (uint32_t)hi[j], (uint32_t)(hi[j] >> 32)});
+                    tot = (s0 + j == 0) ? v : tot + v;
+                }
+        }
+        *reinterpret_cast<u2*>(y + (size_t)m * N + nn) = pack_f16x4(tot);
     }
-    if (tid == 0) atomicExch(&counters[tile], 0);
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------------- prefill
@@ -284,13 +344,26 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
     return hipGetLastError();
 }
 
-template <int KS>
-static hipError_t launch_decode(const w4a16_plan& p, const u4* Wp, const uint16_t* x,
-                                const uint16_t* s, uint16_t* y, float* ws, int* cnt, hipStream_t st) {
+template <int NBW, int WAVES, int D>
+static hipError_t launch_decode_t(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
+                                  uint16_t* y, float* ws, int* cnt, hipStream_t st) {
     const int gshift = p.G == 128 ? 1 : 0;
-    hipLaunchKernelGGL((decode_kernel<kDecodeWaves, KS>), dim3(p.grid), dim3(kDecodeWaves * 64), 0, st,
-                       Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits);
+    hipLaunchKernelGGL((decode_kernel<NBW, WAVES, D>), dim3(p.grid), dim3(WAVES * 64), 0, st,
+                       Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
     return hipGetLastError();
+}
+
+static hipError_t launch_decode(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
+                                uint16_t* y, float* ws, int* cnt, hipStream_t st) {
+    // decode_variant packs (NBW, WAVES, D); the planner only emits entries of kDecodeTable.
+    switch (p.decode_variant) {
+#define W4A16_DEC_CASE(I) \
+        case I: return launch_decode_t<kDecodeTable[I].nbw, kDecodeTable[I].waves, kDecodeTable[I].depth>(p, Wp, x, s, y, ws, cnt, st);
+        W4A16_DEC_CASE(0) W4A16_DEC_CASE(1) W4A16_DEC_CASE(2) W4A16_DEC_CASE(3)
+        W4A16_DEC_CASE(4) W4A16_DEC_CASE(5) W4A16_DEC_CASE(6) W4A16_DEC_CASE(7)
+#undef W4A16_DEC_CASE
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace w4a16
@@ -311,12 +384,7 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
     if (p.kernel == W4A16_VARIANT_DECODE) {
         float* ws = reinterpret_cast<float*>(workspace);
         int* cnt = reinterpret_cast<int*>(counters);
-        switch (p.slab_chunks) {
-            case 4:  e = launch_decode<4>(p, wp, x, scales, y, ws, cnt, st); break;
-            case 8:  e = launch_decode<8>(p, wp, x, scales, y, ws, cnt, st); break;
-            case 16: e = launch_decode<16>(p, wp, x, scales, y, ws, cnt, st); break;
-            default: return W4A16_ERR_INVALID;
-        }
+        e = launch_decode(p, wp, x, scales, y, ws, cnt, st);
     } else {
         switch (p.kernel) {
             case 1: e = launch_prefill<1>(p, wp, x, scales, y, st); break;

@@ -126,37 +126,65 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
     out.M = M; out.N = N; out.K = K; out.G = G;
 
     if (v == 0) {
-        // Decode: 64-column tiles x K slabs of KS chunks.  Pick the largest slab that still
-        // gives >= 4 workgroups per CU (memory-level parallelism); otherwise the smallest slab.
+        // Decode.  Column tiles of 16*NBW channels; the workgroup's WAVES waves split its K
+        // range (kcw chunks each); `splits` workgroups split K further only when there are too
+        // few column tiles to give every CU a workgroup.  NBW grows with M so that the x
+        // fragments each wave loads stay below ~2x its weight bytes.
         const int KC = K / 64;
-        const int ntiles = N / kDecodeTileN;
         const int cus = lim->cu_count > 0 ? lim->cu_count : 1;
-        const int cand[3] = {16, 8, 4};
-        int ks = 0;
-        for (int i = 0; i < 3; ++i) {
-            const int c = cand[i];
-            if (KC % c || decode_lds_bytes(c) > lim->lds_bytes_per_block) continue;
-            if (kDecodeWaves * 64 > lim->max_threads_per_block) continue;
-            ks = c;                                           // smallest valid so far
-            if ((int64_t)ntiles * (KC / c) >= 4LL * cus) break;
+        int var = -1, splits = 0;
+        if (const char* o = std::getenv("W4A16_DECODE")) {          // tuning override "v,splits"
+            int ov = -1, os = 0;
+            if (std::sscanf(o, "%d,%d", &ov, &os) == 2 && ov >= 0 && ov < kNumDecodeCfg && os >= 1 &&
+                KC % (os * kDecodeTable[ov].waves) == 0) { var = ov; splits = os; }
         }
-        if (!ks)
+        if (var < 0) {
+            // Shapes measured fastest on MI355X for the Llama-3 decode projections: wide column
+            // tiles (4 n16 blocks) without split when N alone fills the device; 8-wave wide
+            // tiles split over K until every CU has a workgroup when N is small and K is long;
+            // single-n16-block tiles with full K for small N and short K.
+            auto ok = [&](int cand, int sp) {
+                return sp >= 1 && KC % (sp * kDecodeTable[cand].waves) == 0;
+            };
+            auto ntiles_of = [&](int cand) { return N / (16 * kDecodeTable[cand].nbw); };
+            if ((int64_t)ntiles_of(7) * 8 >= 7LL * cus && ok(7, 1)) {
+                var = 7; splits = 1;
+            } else if (KC >= 128) {
+                for (int sp = 1; sp <= KC; ++sp)
+                    if (ok(6, sp) && ((int64_t)ntiles_of(6) * sp >= cus || KC / (sp * 8) <= 4)) {
+                        var = 6; splits = sp; break;
+                    }
+            } else {
+                const int cand = M <= 4 ? 0 : 4;
+                if (ok(cand, 1)) { var = cand; splits = 1; }
+            }
+            if (var < 0) {                                               // any valid shape
+                for (int cand = 0; cand < kNumDecodeCfg && var < 0; ++cand)
+                    for (int sp = 1; sp <= KC; ++sp)
+                        if (ok(cand, sp)) { var = cand; splits = sp; break; }
+            }
+        }
+        if (var < 0 || decode_lds_bytes(var) > lim->lds_bytes_per_block ||
+            kDecodeTable[var].waves * 64 > lim->max_threads_per_block)
             return fail(W4A16_ERR_NO_CONFIG, err, errlen, "no pipeline configuration fits in %d B of shared memory",
                         lim->lds_bytes_per_block);
-        int splits = KC / ks;
-        if (ntiles > kMaxCounterSlots) { ks = 0; }
-        if (!ks) return fail(W4A16_ERR_NO_CONFIG, err, errlen, "N too large for the decode kernel");
+        const DecodeCfg& c = kDecodeTable[var];
+        const int ntiles = N / (16 * c.nbw);
+        if (splits > 1 && ntiles > kMaxCounterSlots)
+            return fail(W4A16_ERR_NO_CONFIG, err, errlen, "N too large for the decode kernel");
         out.kernel = 0;
-        out.slab_chunks = ks;
+        out.decode_variant = var;
+        out.slab_chunks = KC / (splits * c.waves);
         out.splits = splits;
-        out.tile_n = kDecodeTileN;
-        out.block = kDecodeWaves * 64;
+        out.tile_n = 16 * c.nbw;
+        out.block = c.waves * 64;
         out.grid = ntiles * splits;
         out.counter_slots = splits > 1 ? ntiles : 0;
         out.workspace_bytes = splits > 1 ? (uint64_t)splits * M * N * sizeof(float) : 0;
         if (debug_enabled())
-            std::fprintf(stderr, "decode dispatch G=%d M=%d N=%d K=%d slab=%d splits=%d grid=%d\n",
-                         G, M, N, K, ks, splits, out.grid);
+            std::fprintf(stderr, "decode dispatch G=%d M=%d N=%d K=%d shape=%d (nbw=%d waves=%d depth=%d) "
+                         "kcw=%d splits=%d grid=%d\n", G, M, N, K, var, c.nbw, c.waves, c.depth,
+                         out.slab_chunks, splits, out.grid);
     } else {
         int cfg = v;                                          // 1..4 forced, or -1 = auto
         if (cfg < 0) cfg = prefill_select(M, N, *lim);

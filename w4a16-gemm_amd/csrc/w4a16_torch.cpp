@@ -117,6 +117,7 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
     d["kernel"] = plan.kernel; d["splits"] = plan.splits; d["slab_chunks"] = plan.slab_chunks;
     d["tile_n"] = plan.tile_n; d["grid"] = plan.grid; d["block"] = plan.block;
     d["counter_slots"] = plan.counter_slots; d["workspace_bytes"] = (uint64_t)plan.workspace_bytes;
+    d["decode_variant"] = plan.decode_variant;
     d["cu_count"] = lim.cu_count; d["gcn_arch"] = lim.gcn_arch; d["lds_bytes_per_block"] = lim.lds_bytes_per_block;
     return d;
 }
