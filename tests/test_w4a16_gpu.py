@@ -347,3 +347,39 @@ def test_decode_split_consistency_large_k():
     ref = ref_gemm(x, q, scales, 128, key)
     assert_close(gemm(Wp, x, scales, variant=0), ref)
     assert_close(gemm(Wp, x, scales, variant=2), ref)
+
+
+# Every decode kernel shape of the planner's table, forced through W4A16_DECODE="v,splits"
+# (read by the planner on each call), on shapes whose K range divides evenly.
+DECODE_FORCED = [
+    # (variant, splits, N, K): register kernels (kind 0), LDS-DMA kernels (kind 1)
+    (0, 1, 256, 4096), (1, 2, 256, 4096), (2, 1, 256, 4096), (3, 4, 256, 4096),
+    (4, 2, 256, 4096), (5, 1, 256, 4096), (6, 8, 256, 4096), (7, 1, 256, 4096),
+    (8, 1, 256, 4096), (9, 1, 256, 4096), (12, 1, 256, 4096), (13, 1, 256, 4096),
+    (14, 2, 256, 4096), (15, 1, 256, 4096),
+    (10, 4, 256, 14336), (11, 2, 256, 14336), (6, 4, 256, 14336), (0, 14, 256, 14336),
+    # streaming ring kernels (kind 2)
+    (16, 1, 256, 4096), (17, 1, 256, 4096), (18, 2, 256, 4096), (19, 1, 256, 4096),
+    (20, 4, 256, 4096), (21, 1, 256, 4096), (22, 1, 256, 4096), (23, 2, 256, 4096),
+    (20, 2, 256, 14336), (16, 7, 256, 14336),
+]
+
+
+@pytest.mark.parametrize("v,splits,N,K", DECODE_FORCED)
+def test_decode_shapes_forced(v, splits, N, K, monkeypatch):
+    torch = torch_cuda()
+    import w4a16_opt
+    monkeypatch.setenv("W4A16_DECODE", f"{v},{splits}")
+    info = w4a16_opt.plan_info(16, N, K, 128, 0)
+    assert info["decode_variant"] == v and info["splits"] == splits, info
+    x, q, scales, Wp, key = make_problem(16, N, K, 128, seed=v + 31)
+    Wd = dequant_f32(key)
+    for M in (1, 5, 16):
+        xm = x[:M].contiguous()
+        assert_close(gemm(Wp, xm, scales, variant=0), ref_gemm(xm, q, scales, 128, key))
+    ks = list(range(0, K, K // 16))[:16]
+    xo = torch.zeros(16, K, dtype=torch.half, device="cuda")
+    xo[torch.arange(16), torch.tensor(ks)] = 1
+    y = gemm(Wp, xo, scales, variant=0).float().cpu().numpy()
+    assert np.array_equal(y, Wd[:, ks].T), f"one-hot mismatch for decode shape {v} splits {splits}"
+    assert torch.equal(gemm(Wp, xo, scales, variant=0), gemm(Wp, xo, scales, variant=0))

@@ -25,23 +25,37 @@ constexpr int kLdsRowBytes = 144;
 constexpr int prefill_lds_bytes(int cfg) { return 2 * kPrefillTable[cfg].bm * kLdsRowBytes; }
 constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n; }
 
-// Decode kernel shapes: NBW n16 blocks (16*NBW output channels) per workgroup, WAVES waves
-// splitting the workgroup's K range, software-pipeline depth D (chunks in flight per wave).
+// Decode kernel shapes.  A workgroup covers NBW n16 blocks (16*NBW output channels) with WAVES
+// waves splitting its K range.
+//   kind 0: decode_kernel         weights streamed into VGPRs, pipeline depth d chunks, any
+//                                  chunk count per wave;
+//   kind 1: decode_lds_kernel     weights by direct-to-LDS loads, all d chunks of a wave at once
+//                                  (exactly d chunks per wave);
+//   kind 2: decode_stream_kernel  per-wave ring of d chunk pairs in LDS (the pairs per wave must
+//                                  be a multiple of d).
 struct DecodeCfg {
-    int nbw, waves, depth;
+    int kind, nbw, waves, d;
 };
-constexpr DecodeCfg kDecodeTable[8] = {
-    {1, 16, 4},   // 0
-    {1, 16, 2},   // 1
-    {2, 16, 4},   // 2
-    {2, 16, 2},   // 3
-    {1, 8, 4},    // 4
-    {2, 8, 4},    // 5
-    {4, 8, 4},    // 6
-    {4, 16, 2},   // 7
+constexpr DecodeCfg kDecodeTable[24] = {
+    {0, 1, 16, 4}, {0, 1, 16, 2}, {0, 2, 16, 4}, {0, 2, 16, 2},     // 0-3
+    {0, 1, 8, 4},  {0, 2, 8, 4},  {0, 4, 8, 4},  {0, 4, 16, 2},     // 4-7
+    {1, 4, 16, 4}, {1, 4, 8, 8},  {1, 4, 8, 7},  {1, 2, 16, 7},     // 8-11
+    {1, 1, 16, 4}, {1, 2, 16, 4}, {1, 2, 8, 4},  {1, 1, 8, 8},      // 12-15
+    {2, 4, 4, 4},  {2, 4, 8, 4},  {2, 2, 4, 4},  {2, 1, 4, 4},      // 16-19
+    {2, 4, 4, 2},  {2, 2, 8, 4},  {2, 1, 8, 4},  {2, 4, 8, 2},      // 20-23
 };
-constexpr int kNumDecodeCfg = 8;
-constexpr int decode_lds_bytes(int v) { return kDecodeTable[v].waves * kDecodeTable[v].nbw * 64 * 16 + 16; }
+constexpr int kNumDecodeCfg = 24;
+constexpr int decode_lds_bytes(int v) {
+    return kDecodeTable[v].kind == 0   ? kDecodeTable[v].waves * kDecodeTable[v].nbw * 64 * 16 + 16
+           : kDecodeTable[v].kind == 1 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * ((kDecodeTable[v].d + 1) / 2) * 1024 + 16
+                                       : kDecodeTable[v].waves * kDecodeTable[v].nbw * kDecodeTable[v].d * 1024 + 16;
+}
+// Whether a decode shape can cover K (in 64-wide chunks) with `splits` workgroups per column tile.
+constexpr bool decode_shape_fits(int v, int KC, int splits) {
+    return splits >= 1 && KC % (splits * kDecodeTable[v].waves) == 0 &&
+           (kDecodeTable[v].kind != 1 || KC == splits * kDecodeTable[v].waves * kDecodeTable[v].d) &&
+           (kDecodeTable[v].kind != 2 || ((KC / (splits * kDecodeTable[v].waves)) % (2 * kDecodeTable[v].d) == 0));
+}
 
 // Counter buffer size (ints) the library may ask for: one per decode column tile.
 constexpr int32_t kMaxCounterSlots = 1 << 18;

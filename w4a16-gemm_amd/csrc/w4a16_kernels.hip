@@ -44,6 +44,74 @@ __device__ __forceinline__ u4 xpose_rows(u4 v) {
     return u4{c[0], c[1], e[0], e[1]};
 }
 
+// Final stage shared by the decode kernels.  Thread (rb, lane) of the first NBW waves holds the
+// workgroup's fp32 result for token li and channels n..n+3 of n16 block nb0+rb (`have`).  With
+// one split it is rounded to fp16 and stored.  Otherwise it is handed to the last workgroup of
+// the column tile through the workspace (see the decode comment above) and summed in split order.
+template <int NBW, int WAVES>
+__device__ __forceinline__ void decode_finish(f4 sum, bool have, int rb, int lane, int split, int tile, int nb0,
+                                              uint16_t* __restrict__ y, float* __restrict__ ws,
+                                              int* __restrict__ counters, int M, int N, int splits) {
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    const int kb = lane >> 4;
+    const int li = lane & 15;
+    const int n = (nb0 + rb) * 16 + 4 * kb;
+    const bool mine = have && li < M;
+    if (splits == 1) {
+        if (mine) *reinterpret_cast<u2*>(y + (size_t)li * N + n) = pack_f16x4(sum);
+        return;
+    }
+    // Split-K hand-off without agent-scope fences (those write back / invalidate the XCD's whole
+    // L2): the partials travel through agent-scope atomic stores/loads, which are coherent at
+    // device scope by themselves, and every wave waits for its stores to complete
+    // (s_waitcnt vmcnt(0)) before the workgroup's counter RMW.
+    if (mine) {
+        unsigned long long* p = reinterpret_cast<unsigned long long*>(ws + ((size_t)split * M + li) * N + n);
+        const u4 bits = __builtin_bit_cast(u4, sum);
+        __hip_atomic_store(p, (unsigned long long)bits.x | ((unsigned long long)bits.y << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 1, (unsigned long long)bits.z | ((unsigned long long)bits.w << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&counters[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    __syncthreads();
+    if (!s_last) return;
+
+    // Last arrival: thread (m, c4) adds the `splits` partials of its 4 channels in split order,
+    // issuing the loads of up to 8 splits at once.
+    constexpr int C4 = NBW * 4;                              // float4 groups per row of the tile
+    if (tid < M * C4) {
+        const int m = tid / C4;
+        const int c4 = tid - m * C4;
+        const int nn = nb0 * 16 + c4 * 4;
+        const unsigned long long* p = reinterpret_cast<const unsigned long long*>(ws + (size_t)m * N + nn);
+        const size_t sstride = (size_t)M * N / 2;           // in 8-byte words
+        f4 tot = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < splits; s0 += 8) {
+            unsigned long long lo[8], hi[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (s0 + j < splits) {
+                    lo[j] = __hip_atomic_load(p + (size_t)(s0 + j) * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    hi[j] = __hip_atomic_load(p + (size_t)(s0 + j) * sstride + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (s0 + j < splits) {
+                    const f4 v = __builtin_bit_cast(f4, u4{(uint32_t)lo[j], (uint32_t)(lo[j] >> 32),
+                                                           (uint32_t)hi[j], (uint32_t)(hi[j] >> 32)});
+                    tot = (s0 + j == 0) ? v : tot + v;
+                }
+        }
+        *reinterpret_cast<u2*>(y + (size_t)m * N + nn) = pack_f16x4(tot);
+    }
+    if (tid == 0) __hip_atomic_store(&counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int NBW, int WAVES, int D>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
@@ -51,7 +119,6 @@ decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
               float* __restrict__ ws, int* __restrict__ counters,
               int M, int N, int K, int gshift, int splits, int kcw) {
     __shared__ __attribute__((aligned(16))) f4 red[WAVES][NBW][64];
-    __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -123,61 +190,353 @@ decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) sum += red[w][rb][lane];
     }
-    // thread (rb, lane) now holds token li, channels n .. n+3 of the workgroup's tile
-    const int n = (nb0 + rb) * 16 + 4 * kb;
-    const bool mine = tid < NBW * 64 && li < M;
-    if (splits == 1) {
-        if (mine) *reinterpret_cast<u2*>(y + (size_t)li * N + n) = pack_f16x4(sum);
-        return;
-    }
-    // Split-K hand-off without agent-scope fences (those write back / invalidate the XCD's whole
-    // L2): the partials travel through agent-scope atomic stores/loads, which are coherent at
-    // device scope by themselves, and every wave waits for its stores to complete
-    // (s_waitcnt vmcnt(0)) before the workgroup's counter RMW.
-    if (mine) {
-        unsigned long long* p = reinterpret_cast<unsigned long long*>(ws + ((size_t)split * M + li) * N + n);
-        const u4 bits = __builtin_bit_cast(u4, sum);
-        __hip_atomic_store(p, (unsigned long long)bits.x | ((unsigned long long)bits.y << 32),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p + 1, (unsigned long long)bits.z | ((unsigned long long)bits.w << 32),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0)
-        s_last = __hip_atomic_fetch_add(&counters[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
-    __syncthreads();
-    if (!s_last) return;
+    decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
+}
 
-    // Last arrival: thread (m, c4) adds the `splits` partials of its 4 channels in split order,
-    // issuing the loads of up to 8 splits at once.
-    constexpr int C4 = NBW * 4;                              // float4 groups per row of the tile
-    if (tid < M * C4) {
-        const int m = tid / C4;
-        const int c4 = tid - m * C4;
-        const int nn = nb0 * 16 + c4 * 4;
-        const unsigned long long* p = reinterpret_cast<const unsigned long long*>(ws + (size_t)m * N + nn);
-        const size_t sstride = (size_t)M * N / 2;           // in 8-byte words
-        f4 tot = {0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < splits; s0 += 8) {
-            unsigned long long lo[8], hi[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (s0 + j < splits) {
-                    lo[j] = __hip_atomic_load(p + (size_t)(s0 + j) * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    hi[j] = __hip_atomic_load(p + (size_t)(s0 + j) * sstride + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (s0 + j < splits) {
-                    const f4 v = __builtin_bit_cast(f4, u4{(uint32_t)lo[j], (uint32_t)(lo[j] >> 32),
-                                                           (uint32_t)hi[j], (uint32_t)(hi[j] >> 32)});
-                    tot = (s0 + j == 0) ? v : tot + v;
-                }
-        }
-        *reinterpret_cast<u2*>(y + (size_t)m * N + nn) = pack_f16x4(tot);
+
+// Decode with the weights streamed by direct-to-LDS loads (global_load_lds_dwordx4): a wave
+// issues every weight chunk of its K range at once without holding them in VGPRs, and without
+// the duplicated 16-byte requests of the register path (lanes i and i+8 read the same word quad
+// back from LDS instead).  Chunks 2p and 2p+1 of one n16 block are 1 KB contiguous in Wp and
+// land contiguously in LDS from one instruction.  The compiler does not order a ds_read after
+// the LDS-DMA that fills it, so the kernel (a) pins the issue order with compiler barriers --
+// x fragments and scales first, then the DMAs pair by pair -- and (b) waits with an explicit
+// s_waitcnt vmcnt(#DMAs issued after pair p) before reading pair p.  Same tiling, reduction
+// and split-K hand-off as decode_kernel; KCW (chunks per wave) is a compile-time constant.
+// s_waitcnt vmcnt(n) for 0 <= n <= 63; n is a constant after unrolling, so this folds to one
+// instruction (larger n would wait for nothing: the kernels never issue more than 63 DMAs).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+        case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+        case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+        case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+        case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+        case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+        case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+        case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+        case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+        case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+        case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+        case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+        case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+        case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+        case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+        case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+        case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+        case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+        case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+        case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+        case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+        case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+        case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+        case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+        case 25: asm volatile("s_waitcnt vmcnt(25)" ::: "memory"); break;
+        case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
+        case 27: asm volatile("s_waitcnt vmcnt(27)" ::: "memory"); break;
+        case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
+        case 29: asm volatile("s_waitcnt vmcnt(29)" ::: "memory"); break;
+        case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
+        case 31: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+        case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
+        case 33: asm volatile("s_waitcnt vmcnt(33)" ::: "memory"); break;
+        case 34: asm volatile("s_waitcnt vmcnt(34)" ::: "memory"); break;
+        case 35: asm volatile("s_waitcnt vmcnt(35)" ::: "memory"); break;
+        case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
+        case 37: asm volatile("s_waitcnt vmcnt(37)" ::: "memory"); break;
+        case 38: asm volatile("s_waitcnt vmcnt(38)" ::: "memory"); break;
+        case 39: asm volatile("s_waitcnt vmcnt(39)" ::: "memory"); break;
+        case 40: asm volatile("s_waitcnt vmcnt(40)" ::: "memory"); break;
+        case 41: asm volatile("s_waitcnt vmcnt(41)" ::: "memory"); break;
+        case 42: asm volatile("s_waitcnt vmcnt(42)" ::: "memory"); break;
+        case 43: asm volatile("s_waitcnt vmcnt(43)" ::: "memory"); break;
+        case 44: asm volatile("s_waitcnt vmcnt(44)" ::: "memory"); break;
+        case 45: asm volatile("s_waitcnt vmcnt(45)" ::: "memory"); break;
+        case 46: asm volatile("s_waitcnt vmcnt(46)" ::: "memory"); break;
+        case 47: asm volatile("s_waitcnt vmcnt(47)" ::: "memory"); break;
+        case 48: asm volatile("s_waitcnt vmcnt(48)" ::: "memory"); break;
+        case 49: asm volatile("s_waitcnt vmcnt(49)" ::: "memory"); break;
+        case 50: asm volatile("s_waitcnt vmcnt(50)" ::: "memory"); break;
+        case 51: asm volatile("s_waitcnt vmcnt(51)" ::: "memory"); break;
+        case 52: asm volatile("s_waitcnt vmcnt(52)" ::: "memory"); break;
+        case 53: asm volatile("s_waitcnt vmcnt(53)" ::: "memory"); break;
+        case 54: asm volatile("s_waitcnt vmcnt(54)" ::: "memory"); break;
+        case 55: asm volatile("s_waitcnt vmcnt(55)" ::: "memory"); break;
+        case 56: asm volatile("s_waitcnt vmcnt(56)" ::: "memory"); break;
+        case 57: asm volatile("s_waitcnt vmcnt(57)" ::: "memory"); break;
+        case 58: asm volatile("s_waitcnt vmcnt(58)" ::: "memory"); break;
+        case 59: asm volatile("s_waitcnt vmcnt(59)" ::: "memory"); break;
+        case 60: asm volatile("s_waitcnt vmcnt(60)" ::: "memory"); break;
+        case 61: asm volatile("s_waitcnt vmcnt(61)" ::: "memory"); break;
+        case 62: asm volatile("s_waitcnt vmcnt(62)" ::: "memory"); break;
+        case 63: asm volatile("s_waitcnt vmcnt(63)" ::: "memory"); break;
+        default: break;
     }
-    if (tid == 0) __hip_atomic_store(&counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Global loads the compiler does not track: the caller orders them with compiler barriers and
+// waits with explicit s_waitcnt vmcnt before reading the result registers.
+__device__ __forceinline__ u4 gload_u4_untracked(const void* p) {
+    u4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ uint32_t gload_u16_untracked(const void* p) {
+    uint32_t v;
+    asm volatile("global_load_ushort %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
+    return v;
+}
+
+// After an explicit wait, re-define the registers of completed untracked loads through an empty
+// asm with in-out operands.  Without this the compiler treats an asm load's result as ready when
+// the asm issues: it may hoist uses above the wait or reuse the register while the load is still
+// in flight (an in-flight load later overwrote a reused address register: a wild address).
+// With it, each result stays live and untouched until the wait and is used only after it.
+template <typename T>
+__device__ __forceinline__ void bind_after_wait(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
+// 16-byte LDS read the compiler does not track (the caller waits with s_waitcnt lgkmcnt(0)
+// and re-binds the result with bind_after_wait).
+__device__ __forceinline__ u4 lds_read_u4(uint32_t addr) {
+    u4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+
+template <int NBW, int WAVES, int KCW>
+__global__ void __launch_bounds__(WAVES * 64)
+decode_lds_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
+                  const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
+                  float* __restrict__ ws, int* __restrict__ counters,
+                  int M, int N, int K, int gshift, int splits) {
+    constexpr int NPAIR = (KCW + 1) / 2;
+    constexpr int WAVE_BYTES = NBW * NPAIR * 1024;          // [n16 block][chunk pair][1 KB]
+    static_assert(NPAIR >= 1 && (NPAIR - 1) * NBW <= 63, "too many DMAs in flight for vmcnt");
+    __shared__ __attribute__((aligned(16))) char wl[WAVES * WAVE_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int kb = lane >> 4;
+    const int li = lane & 15;
+    const int split = blockIdx.x % splits;
+    const int tile = blockIdx.x / splits;
+    const int KC = K >> 6;
+    const int kc0 = (split * WAVES + wave) * KCW;
+    const int nb0 = tile * NBW;
+    const int lanep = ((li & 7) << 2) | kb;
+    char* wreg = wl + wave * WAVE_BYTES;
+
+    // 1. x fragments and scales of all KCW chunks, issued through asm so that the compiler does
+    //    not wait for them (it would wait with vmcnt(0), i.e. for every DMA as well).
+    const uint16_t* xsrc = x + (size_t)min(li, M - 1) * K + (size_t)kc0 * 64 + kb * 8;
+    u4 xq[KCW][2];
+#pragma unroll
+    for (int c = 0; c < KCW; ++c) {
+        xq[c][0] = gload_u4_untracked(xsrc + (size_t)c * 64);
+        xq[c][1] = gload_u4_untracked(xsrc + (size_t)c * 64 + 32);
+    }
+    uint32_t sq[NBW][KCW];
+#pragma unroll
+    for (int b = 0; b < NBW; ++b)
+#pragma unroll
+        for (int c = 0; c < KCW; ++c)
+            sq[b][c] = gload_u16_untracked(scales + (size_t)((kc0 + c) >> gshift) * N + (size_t)(nb0 + b) * 16 + li);
+    asm volatile("" ::: "memory");
+
+    // 2. weight DMAs, pair by pair (lanes 0-31: chunk 2p, lanes 32-63: chunk 2p+1).
+#pragma unroll
+    for (int p = 0; p < NPAIR; ++p)
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) {
+            const u4* src = Wp + ((size_t)(nb0 + b) * KC + kc0 + 2 * p) * 32 + lane;
+            auto* dst = (__attribute__((address_space(3))) void*)(wreg + (b * NPAIR + p) * 1024);
+            if (2 * p + 1 < KCW || lane < 32) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+        }
+    asm volatile("" ::: "memory");
+
+    // 3. dequantise + MFMA in K order, waiting for each pair's DMAs.  The LDS reads of DMA'd
+    //    data are issued through asm (lds_read_u4) so that the only waits are the explicit ones.
+    const Dq d = dq_setup(lane);
+    const uint32_t wbase_lane = (uint32_t)reinterpret_cast<uintptr_t>(wreg) + lanep * 16;
+    f4 acc[NBW];
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < NPAIR; ++p) {
+        wait_vmcnt((NPAIR - 1 - p) * NBW);
+        if (p == 0) {                       // x and scales were issued before every DMA
+#pragma unroll
+            for (int c = 0; c < KCW; ++c) { bind_after_wait(xq[c][0]); bind_after_wait(xq[c][1]); }
+#pragma unroll
+            for (int b = 0; b < NBW; ++b)
+#pragma unroll
+                for (int c = 0; c < KCW; ++c) bind_after_wait(sq[b][c]);
+        }
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int c = 2 * p + cc;
+            if (c >= KCW) break;
+            const h8 b0 = __builtin_bit_cast(h8, xpose_rows(xq[c][0]));
+            const h8 b1 = __builtin_bit_cast(h8, xpose_rows(xq[c][1]));
+            u4 wv[NBW];
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) wv[b] = lds_read_u4(wbase_lane + (b * NPAIR + p) * 1024 + cc * 512);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) bind_after_wait(wv[b]);
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) {
+                const u4 w = wv[b];
+                const h2 s2 = scale2((uint16_t)sq[b][c]);
+                acc[b] = mfma16x16x32(dq_frag(w.x, w.y, d, s2), b0, acc[b]);
+                acc[b] = mfma16x16x32(dq_frag(w.z, w.w, d, s2), b1, acc[b]);
+            }
+        }
+    }
+
+    // 4. cross-wave reduction in wave order; each wave parks its tile in its own LDS region.
+    f4* red = reinterpret_cast<f4*>(wreg);
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) red[b * 64 + lane] = acc[b];
+    __syncthreads();
+    f4 sum = {0.f, 0.f, 0.f, 0.f};
+    const int rb = tid >> 6;
+    if (tid < NBW * 64) {
+        sum = reinterpret_cast<const f4*>(wl)[rb * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) sum += reinterpret_cast<const f4*>(wl + w * WAVE_BYTES)[rb * 64 + lane];
+    }
+    decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
+}
+
+
+// Decode with a per-wave software pipeline over a ring of D chunk pairs in LDS.  Each wave walks
+// a long K range (kcw chunks, kcw even) pair by pair: while it dequantises and multiplies pair p,
+// pairs p+1..p+D-1 are in flight (weights by direct-to-LDS loads, x fragments and scales by
+// untracked VGPR loads), and pair p+D is issued into the slot it just consumed.  Compute thus
+// follows the memory stream instead of waiting for a wave's whole range.  Issue order per pair is
+// x, scales, then the NBW weight DMAs (OPS operations), so waiting for pair p is
+// s_waitcnt vmcnt(OPS * #pairs issued after p).  Reduction and split-K hand-off as above.
+template <int NBW, int WAVES, int D>
+__global__ void __launch_bounds__(WAVES * 64)
+decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
+                     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
+                     float* __restrict__ ws, int* __restrict__ counters,
+                     int M, int N, int K, int gshift, int splits, int kcw) {
+    constexpr int SLOT = NBW * 1024;                         // [n16 block][2 chunks][512 B]
+    constexpr int WAVE_BYTES = D * SLOT;
+    constexpr int OPS = 4 + 2 * NBW + NBW;                   // x loads + scale loads + DMAs per pair
+    static_assert((D - 1) * OPS <= 63, "too many loads in flight for vmcnt");
+    __shared__ __attribute__((aligned(16))) char wl[WAVES * WAVE_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int kb = lane >> 4;
+    const int li = lane & 15;
+    const int split = blockIdx.x % splits;
+    const int tile = blockIdx.x / splits;
+    const int KC = K >> 6;
+    const int kc0 = (split * WAVES + wave) * kcw;
+    const int nb0 = tile * NBW;
+    const int lanep = ((li & 7) << 2) | kb;
+    const int npair = kcw >> 1;
+    char* wreg = wl + wave * WAVE_BYTES;
+    const uint32_t wlds = (uint32_t)reinterpret_cast<uintptr_t>(wreg) + lanep * 16;
+
+    const uint16_t* xsrc = x + (size_t)min(li, M - 1) * K + (size_t)kc0 * 64 + kb * 8;
+    const u4* wsrc = Wp + ((size_t)nb0 * KC + kc0) * 32 + lane;
+    const uint16_t* ssrc = scales + (size_t)nb0 * 16 + li;
+
+    u4 xq[D][4];                                             // chunk 2p: h0, h1; chunk 2p+1: h0, h1
+    uint32_t sq[D][NBW][2];
+    auto issue = [&](int p, int slot) {
+        const int c = 2 * p;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xq[slot][j] = gload_u4_untracked(xsrc + (size_t)c * 64 + 32 * j);
+#pragma unroll
+        for (int b = 0; b < NBW; ++b)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                sq[slot][b][j] = gload_u16_untracked(ssrc + (size_t)((kc0 + c + j) >> gshift) * N + b * 16);
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) {
+            auto* dst = (__attribute__((address_space(3))) void*)(wreg + slot * SLOT + b * 1024);
+            __builtin_amdgcn_global_load_lds(wsrc + (size_t)b * KC * 32 + (size_t)c * 32, dst, 16, 0, 0);
+        }
+        asm volatile("" ::: "memory");
+    };
+
+    const Dq d = dq_setup(lane);
+    f4 acc[NBW];
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // Consume ring slot s (pair p): x/scales/weights of the pair are complete when this runs.
+    auto consume = [&](int s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bind_after_wait(xq[s][j]);
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) { bind_after_wait(sq[s][b][0]); bind_after_wait(sq[s][b][1]); }
+        u4 wv[2][NBW];
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) wv[cc][b] = lds_read_u4(wlds + s * SLOT + b * 1024 + cc * 512);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) bind_after_wait(wv[cc][b]);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const h8 b0 = __builtin_bit_cast(h8, xpose_rows(xq[s][2 * cc]));
+            const h8 b1 = __builtin_bit_cast(h8, xpose_rows(xq[s][2 * cc + 1]));
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) {
+                const h2 s2 = scale2((uint16_t)sq[s][b][cc]);
+                acc[b] = mfma16x16x32(dq_frag(wv[cc][b].x, wv[cc][b].y, d, s2), b0, acc[b]);
+                acc[b] = mfma16x16x32(dq_frag(wv[cc][b].z, wv[cc][b].w, d, s2), b1, acc[b]);
+            }
+        }
+    };
+
+    // Straight-line prologue (npair >= D, npair % D == 0: enforced by the planner), a steady-state
+    // loop that always has D-1 pairs in flight behind the one it consumes, and a straight-line
+    // epilogue that drains the ring.  Every wait count is a compile-time constant.
+#pragma unroll
+    for (int s = 0; s < D; ++s) issue(s, s);
+    for (int p0 = 0; p0 + D < npair; p0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            wait_vmcnt((D - 1) * OPS);
+            consume(s);
+            issue(p0 + D + s, s);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        wait_vmcnt((D - 1 - s) * OPS);
+        consume(s);
+    }
+
+    // Cross-wave reduction in wave order; each wave parks its tile in its own LDS region.
+    f4* red = reinterpret_cast<f4*>(wreg);
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) red[b * 64 + lane] = acc[b];
+    __syncthreads();
+    f4 sum = {0.f, 0.f, 0.f, 0.f};
+    const int rb = tid >> 6;
+    if (tid < NBW * 64) {
+        sum = reinterpret_cast<const f4*>(wl)[rb * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) sum += reinterpret_cast<const f4*>(wl + w * WAVE_BYTES)[rb * 64 + lane];
+    }
+    decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
 }
 
 // ----------------------------------------------------------------------------------- prefill
@@ -344,23 +703,34 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
     return hipGetLastError();
 }
 
-template <int NBW, int WAVES, int D>
-static hipError_t launch_decode_t(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
+template <int V>
+static hipError_t launch_decode_v(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
                                   uint16_t* y, float* ws, int* cnt, hipStream_t st) {
+    constexpr DecodeCfg c = kDecodeTable[V];
     const int gshift = p.G == 128 ? 1 : 0;
-    hipLaunchKernelGGL((decode_kernel<NBW, WAVES, D>), dim3(p.grid), dim3(WAVES * 64), 0, st,
-                       Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
+    if constexpr (c.kind == 0) {
+        hipLaunchKernelGGL((decode_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
+                           Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
+    } else if constexpr (c.kind == 2) {
+        hipLaunchKernelGGL((decode_stream_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
+                           Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
+    } else {
+        hipLaunchKernelGGL((decode_lds_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
+                           Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits);
+    }
     return hipGetLastError();
 }
 
 static hipError_t launch_decode(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
                                 uint16_t* y, float* ws, int* cnt, hipStream_t st) {
-    // decode_variant packs (NBW, WAVES, D); the planner only emits entries of kDecodeTable.
-    switch (p.decode_variant) {
-#define W4A16_DEC_CASE(I) \
-        case I: return launch_decode_t<kDecodeTable[I].nbw, kDecodeTable[I].waves, kDecodeTable[I].depth>(p, Wp, x, s, y, ws, cnt, st);
+    switch (p.decode_variant) {   // the planner only emits entries of kDecodeTable
+#define W4A16_DEC_CASE(I) case I: return launch_decode_v<I>(p, Wp, x, s, y, ws, cnt, st);
         W4A16_DEC_CASE(0) W4A16_DEC_CASE(1) W4A16_DEC_CASE(2) W4A16_DEC_CASE(3)
         W4A16_DEC_CASE(4) W4A16_DEC_CASE(5) W4A16_DEC_CASE(6) W4A16_DEC_CASE(7)
+        W4A16_DEC_CASE(8) W4A16_DEC_CASE(9) W4A16_DEC_CASE(10) W4A16_DEC_CASE(11)
+        W4A16_DEC_CASE(12) W4A16_DEC_CASE(13) W4A16_DEC_CASE(14) W4A16_DEC_CASE(15)
+        W4A16_DEC_CASE(16) W4A16_DEC_CASE(17) W4A16_DEC_CASE(18) W4A16_DEC_CASE(19)
+        W4A16_DEC_CASE(20) W4A16_DEC_CASE(21) W4A16_DEC_CASE(22) W4A16_DEC_CASE(23)
 #undef W4A16_DEC_CASE
         default: return hipErrorInvalidValue;
     }

@@ -135,17 +135,17 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
         int var = -1, splits = 0;
         if (const char* o = std::getenv("W4A16_DECODE")) {          // tuning override "v,splits"
             int ov = -1, os = 0;
-            if (std::sscanf(o, "%d,%d", &ov, &os) == 2 && ov >= 0 && ov < kNumDecodeCfg && os >= 1 &&
-                KC % (os * kDecodeTable[ov].waves) == 0) { var = ov; splits = os; }
+            if (std::sscanf(o, "%d,%d", &ov, &os) == 2 && ov >= 0 && ov < kNumDecodeCfg &&
+                decode_shape_fits(ov, KC, os)) {
+                var = ov; splits = os;
+            }
         }
         if (var < 0) {
             // Shapes measured fastest on MI355X for the Llama-3 decode projections: wide column
             // tiles (4 n16 blocks) without split when N alone fills the device; 8-wave wide
             // tiles split over K until every CU has a workgroup when N is small and K is long;
             // single-n16-block tiles with full K for small N and short K.
-            auto ok = [&](int cand, int sp) {
-                return sp >= 1 && KC % (sp * kDecodeTable[cand].waves) == 0;
-            };
+            auto ok = [&](int cand, int sp) { return decode_shape_fits(cand, KC, sp); };
             auto ntiles_of = [&](int cand) { return N / (16 * kDecodeTable[cand].nbw); };
             if ((int64_t)ntiles_of(7) * 8 >= 7LL * cus && ok(7, 1)) {
                 var = 7; splits = 1;
@@ -160,6 +160,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             }
             if (var < 0) {                                               // any valid shape
                 for (int cand = 0; cand < kNumDecodeCfg && var < 0; ++cand)
+                    if (kDecodeTable[cand].kind == 0)
                     for (int sp = 1; sp <= KC; ++sp)
                         if (ok(cand, sp)) { var = cand; splits = sp; break; }
             }
@@ -174,7 +175,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             return fail(W4A16_ERR_NO_CONFIG, err, errlen, "N too large for the decode kernel");
         out.kernel = 0;
         out.decode_variant = var;
-        out.slab_chunks = KC / (splits * c.waves);
+        out.slab_chunks = KC / (splits * c.waves);             // chunks per wave
         out.splits = splits;
         out.tile_n = 16 * c.nbw;
         out.block = c.waves * 64;
@@ -183,7 +184,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
         out.workspace_bytes = splits > 1 ? (uint64_t)splits * M * N * sizeof(float) : 0;
         if (debug_enabled())
             std::fprintf(stderr, "decode dispatch G=%d M=%d N=%d K=%d shape=%d (nbw=%d waves=%d depth=%d) "
-                         "kcw=%d splits=%d grid=%d\n", G, M, N, K, var, c.nbw, c.waves, c.depth,
+                         "kcw=%d splits=%d grid=%d\n", G, M, N, K, var, c.nbw, c.waves, c.d,
                          out.slab_chunks, splits, out.grid);
     } else {
         int cfg = v;                                          // 1..4 forced, or -1 = auto
