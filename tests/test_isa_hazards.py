@@ -1,6 +1,6 @@
 """CPU check of the gfx950 assembly of the decode kernels (compiled here with hipcc -S).
 
-decode_lds_kernel and decode_stream_kernel issue some loads through inline asm (global_load_* into VGPRs, ds_read_b128)
+decode_lds_kernel, decode_stream_kernel and decode_ring_kernel issue some loads through inline asm (global_load_* into VGPRs, ds_read_b128)
 so that the compiler's conservative waits do not serialise the weight stream.  The compiler does
 not know those registers are written asynchronously, so the kernel re-binds them after each
 explicit wait.  This test proves, for every instantiation, that no instruction reads or writes a
@@ -159,8 +159,8 @@ def _kernels(text):
 
 def test_untracked_load_registers_untouched_until_waited(isa):
     ks = _kernels(isa)
-    lds = [k for k in ks if "decode_lds_kernel" in k or "decode_stream_kernel" in k]
-    assert len(lds) >= 16, list(ks)
+    lds = [k for k in ks if "decode_lds_kernel" in k or "decode_stream_kernel" in k or "decode_ring_kernel" in k]
+    assert len(lds) >= 16 + 20, list(ks)
     problems = {k: check_kernel(ks[k]) for k in lds}
     bad = {k: v[:5] for k, v in problems.items() if v}
     assert not bad, bad
@@ -174,6 +174,18 @@ def test_checker_flags_a_hoisted_use():
     ok = [";;#ASMSTART", "global_load_dwordx4 v[2:5], v[8:9], off", ";;#ASMEND",
           ";;#ASMSTART", "s_waitcnt vmcnt(0)", ";;#ASMEND", "v_permlane32_swap_b32_e32 v2, v4"]
     assert not check_kernel(ok)
+
+
+def test_no_bit_cast_of_vector_element():
+    """clang (ROCm 7.2) lowers __builtin_bit_cast(T, v.y) as a load from &v, i.e. it reads v.x;
+    the device sources must copy a vector element to a scalar before bit-casting it."""
+    bad = []
+    for name in os.listdir(CSRC):
+        if name.endswith((".hip", ".h")):
+            for i, line in enumerate(open(os.path.join(CSRC, name)), 1):
+                if re.search(r"__builtin_bit_cast\([^,]+,\s*[\w\[\]]+(\.[xyzw]|\[\d+\])\s*\)", line):
+                    bad.append(f"{name}:{i}: {line.strip()}")
+    assert not bad, bad
 
 
 def test_no_kernel_spills(isa):

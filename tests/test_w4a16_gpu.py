@@ -363,23 +363,54 @@ DECODE_FORCED = [
     (20, 4, 256, 4096), (21, 1, 256, 4096), (22, 1, 256, 4096), (23, 2, 256, 4096),
     (20, 2, 256, 14336), (16, 7, 256, 14336),
 ]
+# refill-ahead ring kernels (kind 3), both group sizes (one or two groups per chunk pair)
+DECODE_FORCED += [(v, sp, N, K) for v, sp, N, K in [
+    (24, 1, 256, 4096), (25, 2, 256, 4096), (26, 1, 256, 4096), (27, 1, 256, 4096),
+    (28, 1, 256, 4096), (29, 1, 256, 4096), (30, 2, 256, 4096),
+    (24, 7, 256, 14336), (27, 1, 256, 14336), (28, 2, 256, 14336), (29, 7, 256, 14336)]]
+DECODE_FORCED_G = [(v, sp, N, K, 128) for v, sp, N, K in DECODE_FORCED] + [
+    (24, 1, 256, 4096, 64), (27, 2, 256, 4096, 64), (26, 1, 512, 2048, 64), (30, 2, 256, 4096, 64),
+    (28, 2, 256, 14336, 64)]
+# shape 31 has no ring that fits LDS for 9..16 token rows: forced only for M <= 8
+DECODE_FORCED_SMALL_M = [(31, 1, 256, 4096, 128), (31, 2, 256, 4096, 64)]
 
 
-@pytest.mark.parametrize("v,splits,N,K", DECODE_FORCED)
-def test_decode_shapes_forced(v, splits, N, K, monkeypatch):
+@pytest.mark.parametrize("v,splits,N,K,G", DECODE_FORCED_G)
+def test_decode_shapes_forced(v, splits, N, K, G, monkeypatch):
     torch = torch_cuda()
     import w4a16_opt
     monkeypatch.setenv("W4A16_DECODE", f"{v},{splits}")
-    info = w4a16_opt.plan_info(16, N, K, 128, 0)
+    info = w4a16_opt.plan_info(16, N, K, G, 0)
     assert info["decode_variant"] == v and info["splits"] == splits, info
-    x, q, scales, Wp, key = make_problem(16, N, K, 128, seed=v + 31)
+    x, q, scales, Wp, key = make_problem(16, N, K, G, seed=v + 31)
     Wd = dequant_f32(key)
-    for M in (1, 5, 16):
+    for M in (1, 3, 5, 9, 16):
         xm = x[:M].contiguous()
-        assert_close(gemm(Wp, xm, scales, variant=0), ref_gemm(xm, q, scales, 128, key))
-    ks = list(range(0, K, K // 16))[:16]
-    xo = torch.zeros(16, K, dtype=torch.half, device="cuda")
-    xo[torch.arange(16), torch.tensor(ks)] = 1
+        assert_close(gemm(Wp, xm, scales, variant=0), ref_gemm(xm, q, scales, G, key))
+    _onehot_decode_check(Wp, scales, Wd, K, v, splits, 16)
+
+
+@pytest.mark.parametrize("v,splits,N,K,G", DECODE_FORCED_SMALL_M)
+def test_decode_shapes_forced_small_m(v, splits, N, K, G, monkeypatch):
+    torch = torch_cuda()
+    import w4a16_opt
+    monkeypatch.setenv("W4A16_DECODE", f"{v},{splits}")
+    info = w4a16_opt.plan_info(8, N, K, G, 0)
+    assert info["decode_variant"] == v and info["splits"] == splits, info
+    assert w4a16_opt.plan_info(16, N, K, G, 0)["decode_variant"] != v    # does not fit: not planned
+    x, q, scales, Wp, key = make_problem(8, N, K, G, seed=v + 37)
+    for M in (1, 4, 8):
+        xm = x[:M].contiguous()
+        assert_close(gemm(Wp, xm, scales, variant=0), ref_gemm(xm, q, scales, G, key))
+    _onehot_decode_check(Wp, scales, dequant_f32(key), K, v, splits, 8)
+
+
+def _onehot_decode_check(Wp, scales, Wd, K, v, splits, m):
+    """x = e_k rows (m of them, spread over K): y must be the dequantised columns, bit-exact."""
+    torch = torch_cuda()
+    ks = list(range(0, K, K // m))[:m]
+    xo = torch.zeros(m, K, dtype=torch.half, device="cuda")
+    xo[torch.arange(m), torch.tensor(ks)] = 1
     y = gemm(Wp, xo, scales, variant=0).float().cpu().numpy()
     assert np.array_equal(y, Wd[:, ks].T), f"one-hot mismatch for decode shape {v} splits {splits}"
     assert torch.equal(gemm(Wp, xo, scales, variant=0), gemm(Wp, xo, scales, variant=0))

@@ -32,29 +32,45 @@ constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m 
 //   kind 1: decode_lds_kernel     weights by direct-to-LDS loads, all d chunks of a wave at once
 //                                  (exactly d chunks per wave);
 //   kind 2: decode_stream_kernel  per-wave ring of d chunk pairs in LDS (the pairs per wave must
-//                                  be a multiple of d).
+//                                  be a multiple of d);
+//   kind 3: decode_ring_kernel    ring of d + 1 chunk-pair slots (weights and x rows), d pairs in
+//                                  flight also while computing; scales of the wave's K range in
+//                                  LDS (pairs per wave >= d, groups per wave * nbw <= 64).
 struct DecodeCfg {
     int kind, nbw, waves, d;
 };
-constexpr DecodeCfg kDecodeTable[24] = {
+constexpr DecodeCfg kDecodeTable[32] = {
     {0, 1, 16, 4}, {0, 1, 16, 2}, {0, 2, 16, 4}, {0, 2, 16, 2},     // 0-3
     {0, 1, 8, 4},  {0, 2, 8, 4},  {0, 4, 8, 4},  {0, 4, 16, 2},     // 4-7
     {1, 4, 16, 4}, {1, 4, 8, 8},  {1, 4, 8, 7},  {1, 2, 16, 7},     // 8-11
     {1, 1, 16, 4}, {1, 2, 16, 4}, {1, 2, 8, 4},  {1, 1, 8, 8},      // 12-15
     {2, 4, 4, 4},  {2, 4, 8, 4},  {2, 2, 4, 4},  {2, 1, 4, 4},      // 16-19
     {2, 4, 4, 2},  {2, 2, 8, 4},  {2, 1, 8, 4},  {2, 4, 8, 2},      // 20-23
+    {3, 4, 4, 2},  {3, 4, 4, 3},  {3, 4, 8, 1},  {3, 1, 8, 2},      // 24-27
+    {3, 2, 4, 2},  {3, 1, 4, 4},  {3, 2, 8, 1},  {3, 4, 4, 4},      // 28-31
 };
-constexpr int kNumDecodeCfg = 24;
-constexpr int decode_lds_bytes(int v) {
+constexpr int kNumDecodeCfg = 32;
+
+// x-row loads per chunk pair of the kind-3 kernel: 4 token rows each.
+constexpr int decode_ring_xd(int M) { return M <= 4 ? 1 : M <= 8 ? 2 : 4; }
+
+constexpr int decode_lds_bytes(int v, int M) {
     return kDecodeTable[v].kind == 0   ? kDecodeTable[v].waves * kDecodeTable[v].nbw * 64 * 16 + 16
            : kDecodeTable[v].kind == 1 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * ((kDecodeTable[v].d + 1) / 2) * 1024 + 16
-                                       : kDecodeTable[v].waves * kDecodeTable[v].nbw * kDecodeTable[v].d * 1024 + 16;
+           : kDecodeTable[v].kind == 2 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * kDecodeTable[v].d * 1024 + 16
+                                       : kDecodeTable[v].waves *
+                                             (2048 + (kDecodeTable[v].d + 1) * (kDecodeTable[v].nbw + decode_ring_xd(M)) * 1024) + 16;
 }
-// Whether a decode shape can cover K (in 64-wide chunks) with `splits` workgroups per column tile.
-constexpr bool decode_shape_fits(int v, int KC, int splits) {
+// Whether a decode shape can cover K (in 64-wide chunks, group size G) with `splits` workgroups
+// per column tile.
+constexpr bool decode_shape_fits(int v, int KC, int splits, int G) {
     return splits >= 1 && KC % (splits * kDecodeTable[v].waves) == 0 &&
            (kDecodeTable[v].kind != 1 || KC == splits * kDecodeTable[v].waves * kDecodeTable[v].d) &&
-           (kDecodeTable[v].kind != 2 || ((KC / (splits * kDecodeTable[v].waves)) % (2 * kDecodeTable[v].d) == 0));
+           (kDecodeTable[v].kind != 2 || ((KC / (splits * kDecodeTable[v].waves)) % (2 * kDecodeTable[v].d) == 0)) &&
+           (kDecodeTable[v].kind != 3 ||
+            ((KC / (splits * kDecodeTable[v].waves)) % 2 == 0 &&
+             KC / (splits * kDecodeTable[v].waves) >= 2 * kDecodeTable[v].d &&
+             (KC / (splits * kDecodeTable[v].waves)) / (G / 64) * kDecodeTable[v].nbw <= 64));
 }
 
 // Counter buffer size (ints) the library may ask for: one per decode column tile.

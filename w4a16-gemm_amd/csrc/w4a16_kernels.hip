@@ -539,6 +539,193 @@ decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
 }
 
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+
+// Decode with a refill-ahead ring of chunk pairs (kind 3).
+//
+// Work split as in decode_stream_kernel: WAVES waves per column tile of NBW n16 blocks, each
+// wave walking its kcw chunks pair by pair.  Differences:
+//  * The ring has D + 1 slots and the loads of pair p + D are issued BEFORE pair p is
+//    dequantised and multiplied, so the memory system always holds D pairs of every wave,
+//    also while the wave computes.
+//  * A pair's x rows (4*XD rows; rows >= M repeat row M-1) arrive in the slot by direct-to-LDS
+//    loads next to the weights, 16-byte segments XOR-swizzled by row so that the B-operand reads
+//    of 16 token rows hit distinct bank groups.  The scales of the wave's whole K range
+//    ([group][block][16 channels]) arrive by two direct-to-LDS loads before the ring starts
+//    (groups * NBW <= 64, checked by the planner).  Per pair the wave issues NBW + XD memory
+//    instructions (4 + 3*NBW in decode_stream_kernel).
+//  * Weight segments are stored transposed (segment (i % 8) + 8*kb of a chunk holds packed lane
+//    4*(i % 8) + kb), so the 16-byte A-operand reads of 8 consecutive lanes are conflict-free.
+// Dequantisation is dq_frag, bit-identical to the reference's fp16 subtract-then-multiply.
+// Every ring load runs with all 64 lanes active (clamped addresses), so each pair is exactly
+// OPS vector-memory instructions and the vmcnt arithmetic is exact.
+template <int NBW, int WAVES, int D, int XD>
+__global__ void __launch_bounds__(WAVES * 64)
+decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
+                   const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
+                   float* __restrict__ ws, int* __restrict__ counters,
+                   int M, int N, int K, int gshift, int splits, int kcw) {
+    constexpr int S = D + 1;                                 // ring slots
+    constexpr int WSLOT = NBW * 1024;                        // [n16 block][chunk][32 x 16 B]
+    constexpr int XSLOT = XD * 1024;                         // [4*XD rows][16 x 16 B]
+    constexpr int SLOT = WSLOT + XSLOT;
+    constexpr int SBYTES = 2048;                             // [group][block][16 halves]
+    constexpr int WAVE_BYTES = SBYTES + S * SLOT;
+    constexpr int OPS = NBW + XD;
+    static_assert((D - 1) * OPS <= 63, "too many loads in flight for vmcnt");
+    static_assert(WAVES >= NBW && WAVE_BYTES >= NBW * 1024, "reduction layout");
+    __shared__ __attribute__((aligned(16))) char wl[WAVES * WAVE_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int kb = lane >> 4;
+    const int li = lane & 15;
+    const int split = blockIdx.x % splits;
+    const int tile = blockIdx.x / splits;
+    const int KC = K >> 6;
+    const int kc0 = (split * WAVES + wave) * kcw;
+    const int nb0 = tile * NBW;
+    const int npair = kcw >> 1;
+    char* wreg = wl + wave * WAVE_BYTES;
+    const uint32_t lds_wave = (uint32_t)reinterpret_cast<uintptr_t>(wreg);
+
+    // Scales of groups g0 .. g0 + ng - 1: lane j of load q fills [group][block][half] entry
+    // e = 64q + j (8 channels), clamped to the last real entry.
+    {
+        const int g0 = kc0 >> gshift;
+        const int last = (kcw >> gshift) * NBW * 2 - 1;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int e = min(64 * q + lane, last);
+            const uint16_t* src = scales + (size_t)(g0 + e / (2 * NBW)) * N + (size_t)(nb0 + (e >> 1) % NBW) * 16 + (e & 1) * 8;
+            __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(wreg + q * 1024),
+                                             16, 0, 0);
+        }
+    }
+
+    // Per-lane sources of the ring loads.  Weights: lane j fills segment j & 31 of chunk j >> 5
+    // with packed lane 4*(seg % 8) + seg / 8.  x: lane j of load q fills row r = (64q + j) / 16,
+    // segment j % 16, with global segment (j % 16) ^ (r % 8) of row min(r, M - 1).
+    const int wseg = lane & 31;
+    const u4* wsrc = Wp + ((size_t)nb0 * KC + kc0 + (lane >> 5)) * 32 + 4 * (wseg & 7) + (wseg >> 3);
+    const uint16_t* xsrc[XD];
+#pragma unroll
+    for (int q = 0; q < XD; ++q) {
+        const int r = (64 * q + lane) >> 4;
+        const int gseg = (lane & 15) ^ (r & 7);
+        xsrc[q] = x + (size_t)min(r, M - 1) * K + (size_t)kc0 * 64 + gseg * 8;
+    }
+    auto issue = [&](int p, int s) {
+        char* sl = wreg + SBYTES + s * SLOT;
+#pragma unroll
+        for (int b = 0; b < NBW; ++b)
+            __builtin_amdgcn_global_load_lds((const void*)(wsrc + (size_t)b * KC * 32 + (size_t)p * 64),
+                                             (__attribute__((address_space(3))) void*)(sl + b * 1024), 16, 0, 0);
+#pragma unroll
+        for (int q = 0; q < XD; ++q)
+            __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * 128),
+                                             (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024), 16, 0, 0);
+        asm volatile("" ::: "memory");
+    };
+
+    // Per-lane LDS read offsets.
+    const int xr = min(li, M - 1);
+    uint32_t xoff[2][2];
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) xoff[cc][h] = WSLOT + xr * 256 + (((cc * 8 + 4 * h + kb) ^ (xr & 7)) << 4);
+    const uint32_t woff = ((li & 7) + 8 * kb) << 4;
+    const uint32_t soff = lds_wave + li * 2;
+    const Dq d = dq_setup(lane);
+
+    f4 acc[NBW];
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // Pair p sits in slot s; its loads (and the scale loads, which are older) are complete.
+    auto consume = [&](int p, int s) {
+        const uint32_t base = lds_wave + SBYTES + s * SLOT;
+        u4 xv[2][2], wv[2][NBW];
+        uint32_t sc[2][NBW];
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) xv[cc][h] = lds_read_u4(base + xoff[cc][h]);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) wv[cc][b] = lds_read_u4(base + b * 1024 + cc * 512 + woff);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int b = 0; b < NBW; ++b)
+                sc[cc][b] = lds_read_u16(soff + ((((2 * p + cc) >> gshift) * NBW + b) << 5));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) bind_after_wait(xv[cc][h]);
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) { bind_after_wait(wv[cc][b]); bind_after_wait(sc[cc][b]); }
+        }
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const h8 b0 = __builtin_bit_cast(h8, xpose_rows(xv[cc][0]));
+            const h8 b1 = __builtin_bit_cast(h8, xpose_rows(xv[cc][1]));
+#pragma unroll
+            for (int b = 0; b < NBW; ++b) {
+                const h2 s2 = scale2((uint16_t)sc[cc][b]);
+                const u4 w = wv[cc][b];
+                acc[b] = mfma16x16x32(dq_frag(w.x, w.y, d, s2), b0, acc[b]);
+                acc[b] = mfma16x16x32(dq_frag(w.z, w.w, d, s2), b1, acc[b]);
+            }
+        }
+    };
+
+    // Prologue: pairs 0..D-1 in slots 0..D-1 (npair >= D, checked by the planner).  Steady
+    // state: wait for pair p (D-1 younger pairs may stay in flight), refill with pair p + D, then
+    // compute pair p.  Drain: the last D pairs with shrinking waits.  The scale loads are older
+    // than pair 0, so the first wait covers them too.
+#pragma unroll
+    for (int s = 0; s < D; ++s) issue(s, s);
+    int sc_ = 0, si = D;                                     // slot of pair p, slot for pair p + D
+    int p = 0;
+    for (; p + D < npair; ++p) {
+        wait_vmcnt((D - 1) * OPS);
+        issue(p + D, si);
+        consume(p, sc_);
+        sc_ = sc_ + 1 == S ? 0 : sc_ + 1;
+        si = si + 1 == S ? 0 : si + 1;
+    }
+#pragma unroll
+    for (int t = 0; t < D; ++t) {
+        wait_vmcnt((D - 1 - t) * OPS);
+        consume(p + t, sc_);
+        sc_ = sc_ + 1 == S ? 0 : sc_ + 1;
+    }
+
+    // Cross-wave reduction in wave order; each wave parks its tile at the start of its region
+    // (its own loads are complete and its LDS reads have returned).
+    f4* red = reinterpret_cast<f4*>(wreg);
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) red[b * 64 + lane] = acc[b];
+    __syncthreads();
+    f4 sum = {0.f, 0.f, 0.f, 0.f};
+    const int rb = tid >> 6;
+    if (tid < NBW * 64) {
+        sum = reinterpret_cast<const f4*>(wl)[rb * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) sum += reinterpret_cast<const f4*>(wl + w * WAVE_BYTES)[rb * 64 + lane];
+    }
+    decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
+}
+
 // ----------------------------------------------------------------------------------- prefill
 // Replaces the reference prefill kernel pf::w4a16_gemm_prefill (src/vectorized/prefill.cuh:27-184).
 //
@@ -714,6 +901,20 @@ static hipError_t launch_decode_v(const w4a16_plan& p, const u4* Wp, const uint1
     } else if constexpr (c.kind == 2) {
         hipLaunchKernelGGL((decode_stream_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
                            Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
+    } else if constexpr (c.kind == 3) {
+        const int xd = decode_ring_xd(p.M);
+#define W4A16_RING(XD)                                                                                   \
+        hipLaunchKernelGGL((decode_ring_kernel<c.nbw, c.waves, c.d, XD>), dim3(p.grid), dim3(c.waves * 64), \
+                           0, st, Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks)
+        // Shapes whose ring does not fit in LDS for 8 or 16 token rows are never planned for them.
+        if (xd == 1) {
+            W4A16_RING(1);
+        } else if (xd == 2) {
+            if constexpr (decode_lds_bytes(V, 8) <= 163840) W4A16_RING(2); else return hipErrorInvalidValue;
+        } else {
+            if constexpr (decode_lds_bytes(V, 16) <= 163840) W4A16_RING(4); else return hipErrorInvalidValue;
+        }
+#undef W4A16_RING
     } else {
         hipLaunchKernelGGL((decode_lds_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
                            Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits);
@@ -731,6 +932,8 @@ static hipError_t launch_decode(const w4a16_plan& p, const u4* Wp, const uint16_
         W4A16_DEC_CASE(12) W4A16_DEC_CASE(13) W4A16_DEC_CASE(14) W4A16_DEC_CASE(15)
         W4A16_DEC_CASE(16) W4A16_DEC_CASE(17) W4A16_DEC_CASE(18) W4A16_DEC_CASE(19)
         W4A16_DEC_CASE(20) W4A16_DEC_CASE(21) W4A16_DEC_CASE(22) W4A16_DEC_CASE(23)
+        W4A16_DEC_CASE(24) W4A16_DEC_CASE(25) W4A16_DEC_CASE(26) W4A16_DEC_CASE(27)
+        W4A16_DEC_CASE(28) W4A16_DEC_CASE(29) W4A16_DEC_CASE(30) W4A16_DEC_CASE(31)
 #undef W4A16_DEC_CASE
         default: return hipErrorInvalidValue;
     }

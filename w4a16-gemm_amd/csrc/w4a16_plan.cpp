@@ -136,25 +136,45 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
         if (const char* o = std::getenv("W4A16_DECODE")) {          // tuning override "v,splits"
             int ov = -1, os = 0;
             if (std::sscanf(o, "%d,%d", &ov, &os) == 2 && ov >= 0 && ov < kNumDecodeCfg &&
-                decode_shape_fits(ov, KC, os)) {
+                decode_shape_fits(ov, KC, os, G) && decode_lds_bytes(ov, M) <= lim->lds_bytes_per_block &&
+                kDecodeTable[ov].waves * 64 <= lim->max_threads_per_block) {
                 var = ov; splits = os;
             }
         }
         if (var < 0) {
-            // Shapes measured fastest on MI355X for the Llama-3 decode projections: wide column
-            // tiles (4 n16 blocks) without split when N alone fills the device; 8-wave wide
-            // tiles split over K until every CU has a workgroup when N is small and K is long;
-            // single-n16-block tiles with full K for small N and short K.
-            auto ok = [&](int cand, int sp) { return decode_shape_fits(cand, KC, sp); };
+            // Shapes measured fastest on MI355X (graph-timed sweep over the whole table) for the
+            // Llama-3 decode projections, tried in order; the first that fits wins:
+            //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): streaming ring
+            //    of 4 blocks x 4 waves, no split;
+            //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves
+            //    (two-block tiles split in two at M > 8, where x traffic per block grows);
+            //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves.
+            auto ok = [&](int cand, int sp) {
+                return decode_shape_fits(cand, KC, sp, G) && decode_lds_bytes(cand, M) <= lim->lds_bytes_per_block &&
+                       kDecodeTable[cand].waves * 64 <= lim->max_threads_per_block;
+            };
             auto ntiles_of = [&](int cand) { return N / (16 * kDecodeTable[cand].nbw); };
-            if ((int64_t)ntiles_of(7) * 8 >= 7LL * cus && ok(7, 1)) {
-                var = 7; splits = 1;
-            } else if (KC >= 128) {
+            struct Cand { int v, sp; };
+            Cand wide[] = {{20, 1}, {7, 1}};
+            Cand longk_small_m[] = {{27, 1}, {30, 2}};
+            Cand longk_large_m[] = {{30, 2}, {27, 1}};
+            Cand shortk_m4[] = {{22, 1}, {27, 1}};
+            Cand shortk[] = {{27, 1}, {29, 1}};
+            Cand* list;
+            int n;
+            if ((int64_t)ntiles_of(20) * 8 >= 7LL * cus) { list = wide; n = 2; }
+            else if (KC >= 128) { list = M <= 8 ? longk_small_m : longk_large_m; n = 2; }
+            else { list = M <= 4 ? shortk_m4 : shortk; n = 2; }
+            for (int i = 0; i < n && var < 0; ++i)
+                if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus) {
+                    var = list[i].v; splits = list[i].sp;
+                }
+            if (var < 0 && KC >= 128) {
                 for (int sp = 1; sp <= KC; ++sp)
                     if (ok(6, sp) && ((int64_t)ntiles_of(6) * sp >= cus || KC / (sp * 8) <= 4)) {
                         var = 6; splits = sp; break;
                     }
-            } else {
+            } else if (var < 0) {
                 const int cand = M <= 4 ? 0 : 4;
                 if (ok(cand, 1)) { var = cand; splits = 1; }
             }
@@ -165,7 +185,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
                         if (ok(cand, sp)) { var = cand; splits = sp; break; }
             }
         }
-        if (var < 0 || decode_lds_bytes(var) > lim->lds_bytes_per_block ||
+        if (var < 0 || decode_lds_bytes(var, M) > lim->lds_bytes_per_block ||
             kDecodeTable[var].waves * 64 > lim->max_threads_per_block)
             return fail(W4A16_ERR_NO_CONFIG, err, errlen, "no pipeline configuration fits in %d B of shared memory",
                         lim->lds_bytes_per_block);
