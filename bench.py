@@ -122,8 +122,10 @@ def bench_decode(torch, gemm, steps, warmup):
             reps.append(time_graph(torch, [g], 4, 1) / (4 * copies))
         us = statistics.median(reps) * 1e3
         b = alg_bytes(M, N, K)
+        import w4a16_opt
         cases.append({"layer": name, "M": M, "N": N, "K": K, "us": round(us, 3),
-                      "GBps": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)})
+                      "GBps": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                      "kernel": w4a16_opt.plan_info(M, N, K, G)["kernel_name"]})
         log(f"decode {name} M={M}: {us:.2f} us  {b / us / 1e3:.0f} GB/s")
     ms = time_graph(torch, graphs, steps, warmup)
     step_bytes = sum(alg_bytes(M, N, K) for _, N, K, M in DECODE_CASES)
@@ -145,7 +147,21 @@ def bench_prefill(torch, gemm, steps, warmup):
     us = ms * 1e3 / steps
     tfs = alg_flops(M, N, K) / (us * 1e-6) / 1e12
     log(f"prefill {name} M={M}: {us:.1f} us  {tfs:.1f} TFLOP/s")
-    return {"us": us, "TFLOPs": tfs, "steps": steps}
+    import w4a16_opt
+    return {"us": us, "TFLOPs": tfs, "steps": steps, "kernel": w4a16_opt.plan_info(M, N, K, G)["kernel_name"]}
+
+
+def bench_copy(torch, steps):
+    """Calibration workload for HBM-traffic counters: an elementwise copy (torch.mul by 1) of a
+    64 MiB fp16 tensor reads and writes exactly 64 MiB per launch."""
+    n = 32 * 2**20
+    a = torch.randn(n, device="cuda").half()
+    b = torch.empty_like(a)
+    for _ in range(steps):
+        torch.mul(a, 1.0, out=b)
+    torch.cuda.synchronize()
+    return {"workload": "copy", "bytes_read_per_launch": 2 * n, "bytes_written_per_launch": 2 * n,
+            "launches": steps}
 
 
 def cpu_baseline(cases, max_seconds=20.0):
@@ -206,7 +222,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode")
+    ap.add_argument("--workload", choices=("decode", "prefill", "copy"), default="decode",
+                    help="copy: HBM-counter calibration kernel (64 MiB elementwise copy), no benchmark line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--json", default=None, help="also write the JSON line to this file")
@@ -225,9 +242,10 @@ def main(argv=None) -> int:
     dev = torch.cuda.get_device_properties(0)
     log(f"device: {dev.name} ({getattr(dev, 'gcnArchName', '?')}), CUs={dev.multi_processor_count}")
 
-    dec = pre = None
-    if a.workload == "decode" or not a.no_prefill:
-        pass
+    if a.workload == "copy":
+        print(json.dumps(bench_copy(torch, a.steps)), flush=True)
+        return 0
+    pre = None
     dec = bench_decode(torch, gemm, a.steps, a.warmup) if a.workload == "decode" else None
     if a.workload == "prefill" or not a.no_prefill:
         pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
@@ -245,7 +263,8 @@ def main(argv=None) -> int:
                        "G": G, "weight_copies_per_shape": dec["copies"], "timing": "HIP graph replay, HIP events"},
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": load_traffic("decode"),
-                         "kernel": "w4a16::decode_kernel", "bytes_per_launch": dec["bytes_per_launch"],
+                         "kernel": " + ".join(sorted({c["kernel"] for c in dec["cases"]})),
+                         "bytes_per_launch": dec["bytes_per_launch"],
                          "avg_launch_us": round(dec["avg_launch_us"], 3)},
             "cases": dec["cases"],
         })
@@ -255,7 +274,7 @@ def main(argv=None) -> int:
                    "config": {"workload": "BASELINE configs[3]: prefill M=2048 K=8192 N=28672 G=128"},
                    "roofline": {"bound": "mfma", "achieved": round(pre["TFLOPs"], 1), "peak": FP16_MFMA_PEAK_TFS,
                                 "unit": "TFLOP/s", "frac": round(pre["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
-                                "traffic": load_traffic("prefill"), "kernel": "w4a16::prefill_kernel",
+                                "traffic": load_traffic("prefill"), "kernel": pre["kernel"],
                                 "flops_per_launch": alg_flops(M, N, K)}}
         if dec is None:
             out.update({"value": pre_obj["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps,

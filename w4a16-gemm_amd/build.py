@@ -58,7 +58,7 @@ def build_ext() -> str:
 
     cxx = os.environ.get("CXX", "g++")
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    incs = [INCLUDE, *ce.include_paths(), sysconfig.get_paths()["include"], os.path.join(ROCM, "include")]
+    incs = [INCLUDE, CSRC, *ce.include_paths(), sysconfig.get_paths()["include"], os.path.join(ROCM, "include")]
     libdirs = [*ce.library_paths(), os.path.join(ROCM, "lib"), HERE]
     tmp = EXT + ".tmp"
     cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",

@@ -16,7 +16,10 @@
 #include <map>
 #include <mutex>
 
+#include <string>
+
 #include "w4a16.h"
+#include "w4a16_internal.h"
 
 namespace {
 
@@ -118,6 +121,17 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
     d["tile_n"] = plan.tile_n; d["grid"] = plan.grid; d["block"] = plan.block;
     d["counter_slots"] = plan.counter_slots; d["workspace_bytes"] = (uint64_t)plan.workspace_bytes;
     d["decode_variant"] = plan.decode_variant;
+    if (plan.kernel == W4A16_VARIANT_DECODE) {
+        static const char* const kinds[] = {"decode_kernel", "decode_lds_kernel", "decode_stream_kernel",
+                                            "decode_ring_kernel"};
+        const w4a16::DecodeCfg& c = w4a16::kDecodeTable[plan.decode_variant];
+        d["kernel_name"] = std::string("w4a16::") + kinds[c.kind] + "<" + std::to_string(c.nbw) + "," +
+                           std::to_string(c.waves) + "," + std::to_string(c.d) + ">";
+    } else {
+        const w4a16::PrefillTile& t = w4a16::kPrefillTable[plan.kernel];
+        d["kernel_name"] = "w4a16::prefill_kernel<" + std::to_string(t.bm) + "," + std::to_string(t.bn) + "," +
+                           std::to_string(t.waves_m) + "," + std::to_string(t.waves_n) + ">";
+    }
     d["cu_count"] = lim.cu_count; d["gcn_arch"] = lim.gcn_arch; d["lds_bytes_per_block"] = lim.lds_bytes_per_block;
     return d;
 }
