@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 4
+        assert 1 <= p.kernel <= 7
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -157,9 +157,41 @@ def test_decode_plan_invariants(lib, M, N, K):
 def test_prefill_plan_invariants(lib, M, N):
     rc, p, err = plan(lib, M=M, N=N, K=4160, G=64)
     assert rc == 0, err
-    tiles = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128)}[p.kernel]
+    tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
     assert p.workspace_bytes == 0 and p.counter_slots == 0
+
+
+PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128)}
+
+
+@pytest.mark.parametrize("M,N,K,want", [
+    (2048, 28672, 8192, 7), (2048, 14336, 4096, 7), (4096, 4096, 4096, 7),   # wide tiles fill the device
+    (2048, 28672, 8256, None),                                               # odd chunk count: classic only
+    (128, 14336, 4096, None)])                                               # too few wide tiles
+def test_prefill_wide_selection(lib, M, N, K, want):
+    rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
+    assert rc == 0, err
+    if want is None:
+        assert 1 <= p.kernel <= 4, p.kernel
+    else:
+        assert p.kernel == want
+    tiles = PREFILL_TILES[p.kernel]
+    assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
+    assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2}[p.kernel]
+
+
+def test_prefill_override(lib, monkeypatch):
+    for cfg in range(1, 8):
+        monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+        rc, p, err = plan(lib, M=2048, N=4096, K=4096, G=128)
+        assert rc == 0 and p.kernel == cfg, (cfg, p.kernel, err)
+    monkeypatch.setenv("W4A16_PREFILL", "5")                  # wide config, odd chunk count: ignored
+    rc, p, err = plan(lib, M=2048, N=4096, K=4160, G=64)
+    assert rc == 0 and 1 <= p.kernel <= 4
+    monkeypatch.setenv("W4A16_PREFILL", "3")                  # a forced variant wins over the override
+    rc, p, err = plan(lib, M=2048, N=4096, K=4096, G=128, variant=2)
+    assert rc == 0 and p.kernel == 2
 
 
 def test_empty_n_plans_nothing(lib):

@@ -414,3 +414,22 @@ def _onehot_decode_check(Wp, scales, Wd, K, v, splits, m):
     y = gemm(Wp, xo, scales, variant=0).float().cpu().numpy()
     assert np.array_equal(y, Wd[:, ks].T), f"one-hot mismatch for decode shape {v} splits {splits}"
     assert torch.equal(gemm(Wp, xo, scales, variant=0), gemm(Wp, xo, scales, variant=0))
+
+
+# Wide-tile prefill configs (5..7, chosen automatically for large problems) forced through
+# W4A16_PREFILL: bit-identical to the reference-API variants and within the reference tolerance,
+# including M and N tails (rows past M and blocks past N load clamped data and are not stored).
+@pytest.mark.parametrize("cfg", [5, 6, 7])
+@pytest.mark.parametrize("M,N,K,G", [(2048, 4096, 4096, 128), (300, 1040, 2048, 64), (129, 272, 1024, 128),
+                                     (17, 16, 256, 64)])
+def test_prefill_wide_configs_bitwise_equal(cfg, M, N, K, G, monkeypatch):
+    torch = torch_cuda()
+    import w4a16_opt
+    monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+    assert "prefill_wide_kernel" in w4a16_opt.plan_info(M, N, K, G)["kernel_name"]
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=cfg)
+    y = gemm(Wp, x, scales)
+    assert torch.equal(y, gemm(Wp, x, scales, variant=4))
+    assert torch.equal(y, gemm(Wp, x, scales, variant=1))
+    assert_close(y, ref_gemm(x, q, scales, G, key))
+    assert torch.equal(gemm(Wp, x[:M // 2 + 1].contiguous(), scales), y[:M // 2 + 1])

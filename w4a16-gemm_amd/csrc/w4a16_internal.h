@@ -5,24 +5,32 @@
 
 namespace w4a16 {
 
-// Prefill tile configurations, variant ids 1..4 (the reference's PfCfg<1..4>,
-// src/vectorized/kernel.cu:59-63, re-tiled for 64-wide wavefronts and 256 CUs).
+// Prefill tile configurations.  Ids 1..4 are the forced variants of the reference API (its
+// PfCfg<1..4>, src/vectorized/kernel.cu:59-63, re-tiled for 64-wide wavefronts and 256 CUs) and
+// run prefill_kernel; ids 5..7 run prefill_wide_kernel (wave tile 128 x 64) and are chosen by the
+// auto planner (or the W4A16_PREFILL override).  All give bit-identical output.
 struct PrefillTile {
-    int bm, bn, waves_m, waves_n;
+    int bm, bn, waves_m, waves_n, wide;
 };
-constexpr PrefillTile kPrefillTable[5] = {
-    {0, 0, 0, 0},
-    {16, 128, 1, 4},    // 1: small batches: 4 waves across N, wave tile 16 x 32
-    {32, 128, 1, 4},    // 2: wave tile 32 x 32
-    {64, 128, 2, 2},    // 3: wave tile 32 x 64
-    {128, 128, 2, 2},   // 4: wave tile 64 x 64
+constexpr PrefillTile kPrefillTable[8] = {
+    {0, 0, 0, 0, 0},
+    {16, 128, 1, 4, 0},     // 1: small batches: 4 waves across N, wave tile 16 x 32
+    {32, 128, 1, 4, 0},     // 2: wave tile 32 x 32
+    {64, 128, 2, 2, 0},     // 3: wave tile 32 x 64
+    {128, 128, 2, 2, 0},    // 4: wave tile 64 x 64
+    {128, 256, 1, 4, 1},    // 5: wave tile 128 x 64, 4 waves across N
+    {256, 128, 2, 2, 1},    // 6: wave tile 128 x 64, 2 x 2 waves
+    {128, 128, 1, 2, 1},    // 7: wave tile 128 x 64, 2 waves
 };
-constexpr int kNumPrefillCfg = 4;
+constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
+constexpr int kNumPrefillTable = 7;      // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;
 
 constexpr int prefill_lds_bytes(int cfg) { return 2 * kPrefillTable[cfg].bm * kLdsRowBytes; }
+// The wide kernels walk K two chunks per iteration.
+constexpr bool prefill_k_ok(int cfg, int K) { return !kPrefillTable[cfg].wide || (K / 64) % 2 == 0; }
 constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n; }
 
 // Decode kernel shapes.  A workgroup covers NBW n16 blocks (16*NBW output channels) with WAVES

@@ -865,6 +865,166 @@ prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     }
 }
 
+// Prefill with large wave tiles (TM = WM/16 token blocks share each dequantised A operand).
+//
+// Same tile walk and MFMA order as prefill_kernel (every accumulator: chunk 0 h 0, chunk 0 h 1,
+// chunk 1 h 0, ...; identical A and B operands), so its output is bit-identical to every other
+// prefill config.  Differences that cut the vector-ALU work per MFMA:
+//  * each A operand (one n16 block, one chunk half) feeds TM = WM/16 MFMAs, so dequantisation
+//    costs 14/TM VALU per MFMA;
+//  * the weights of chunk kc+2 are loaded while chunk kc is multiplied, into two named register
+//    sets used alternately (the loop is unrolled by two chunks, K/64 must be even), so no
+//    register copies;
+//  * rows past M and blocks past N load clamped, in-bounds data instead of branching (their
+//    results are never stored and rows never mix);
+//  * XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so block b is
+//    given tile (b % 8) * (G / 8) + b / 8: each XCD walks consecutive tiles, i.e. the M tiles
+//    that share a weight tile, through its own L2.
+template <int BM, int BN, int WAVES_M, int WAVES_N>
+__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
+prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
+                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
+                    int M, int N, int K, int gshift, int tiles_m) {
+    constexpr int NT = WAVES_M * WAVES_N * 64;
+    constexpr int WM = BM / WAVES_M;
+    constexpr int WN = BN / WAVES_N;
+    constexpr int TM = WM / 16;
+    constexpr int TN = WN / 16;
+    constexpr int XBUF = BM * kXRow;
+    constexpr int SEGS = BM * 8;
+    constexpr int SPT = SEGS / NT;
+    static_assert(WM % 16 == 0 && WN % 16 == 0 && SEGS % NT == 0, "tile shape");
+    __shared__ __attribute__((aligned(16))) char xs[2 * XBUF];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);      // wave-uniform (SGPR)
+    const int wm = wave / WAVES_N;
+    const int wn = wave - wm * WAVES_N;
+    const int kb = lane >> 4;
+    const int li = lane & 15;
+
+    // XCD-aware tile order (a bijection on [0, gridDim.x)).
+    const int G = gridDim.x;
+    const int G8 = G >> 3;
+    const int b = blockIdx.x;
+    const int tile = b < (G8 << 3) ? (b & 7) * G8 + (b >> 3) : b;
+    const int tm = tile % tiles_m;
+    const int tn = tile / tiles_m;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    const int KC = K >> 6;
+    const int NBLK = N >> 4;
+    const int nb0 = (n0 >> 4) + wn * TN;
+    const int lanep = ((li & 7) << 2) | kb;
+
+    // Wave-uniform bases (SGPRs) plus 32-bit per-lane offsets keep the address registers few.
+    const u4* wbase[TN];
+    const uint16_t* sbase[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int nbc = min(nb0 + j, NBLK - 1);
+        wbase[j] = Wp + (size_t)nbc * KC * 32;
+        sbase[j] = scales + (size_t)nbc * 16;
+    }
+    const uint16_t* xbase = x + (size_t)m0 * K;
+    uint32_t xoff[SPT];                                        // halves, relative to row m0
+#pragma unroll
+    for (int r = 0; r < SPT; ++r) {
+        const int sg = tid + r * NT;
+        xoff[r] = (uint32_t)(min(m0 + (sg >> 3), M - 1) - m0) * (uint32_t)K + (sg & 7) * 8;
+    }
+
+    u4 xr0[SPT], xr1[SPT];
+    auto load_x = [&](int kc, u4 (&xr)[SPT]) {
+        const uint32_t kcl = (uint32_t)min(kc, KC - 1);       // past the end: harmless reload
+#pragma unroll
+        for (int r = 0; r < SPT; ++r) xr[r] = *reinterpret_cast<const u4*>(xbase + xoff[r] + kcl * 64);
+    };
+    auto store_x = [&](int buf, const u4 (&xr)[SPT]) {
+#pragma unroll
+        for (int r = 0; r < SPT; ++r) {
+            const int sg = tid + r * NT;
+            lds_store_xseg(xs + buf * XBUF + (sg >> 3) * kXRow, sg & 7, xr[r]);
+        }
+    };
+    u4 w0[TN], w1[TN];
+    uint16_t s0[TN], s1[TN];
+    auto load_w = [&](int kc, u4 (&w)[TN], uint16_t (&s)[TN]) {
+        const int kcl = min(kc, KC - 1);                     // past the end: harmless reload
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            w[j] = wbase[j][(uint32_t)kcl * 32 + lanep];
+            s[j] = sbase[j][(uint32_t)(kcl >> gshift) * (uint32_t)N + li];
+        }
+    };
+
+    f4 acc[TM][TN];
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[t][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const Dq d = dq_setup(lane);
+    const char* xrow = xs + (wm * WM + li) * kXRow + kb * 16;
+    // One chunk: for each half h, all TM B operands are read from LDS first (one wait, not one
+    // per token block), the TN A operands are dequantised, then the TM x TN MFMAs run.
+    auto compute = [&](int buf, const u4 (&w)[TN], const uint16_t (&s)[TN]) {
+        const char* xb = xrow + buf * XBUF;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            h8 bf[TM];
+#pragma unroll
+            for (int t = 0; t < TM; ++t) bf[t] = *reinterpret_cast<const h8*>(xb + t * 16 * kXRow + h * 64);
+            h8 a[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                a[j] = h ? dq_frag(w[j].z, w[j].w, d, scale2(s[j])) : dq_frag(w[j].x, w[j].y, d, scale2(s[j]));
+#pragma unroll
+            for (int t = 0; t < TM; ++t)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[t][j] = mfma16x16x32(a[j], bf[t], acc[t][j]);
+        }
+    };
+
+    load_x(0, xr0);
+    load_x(1, xr1);
+    load_w(0, w0, s0);
+    load_w(1, w1, s1);
+    store_x(0, xr0);
+    load_x(2, xr0);
+    __syncthreads();
+    // Two chunks per loop trip.  Chunk kc: its x is in LDS buffer kc & 1 and its weights in
+    // register set kc & 1; x of chunk kc+1 (in the other x register set) is written to the other
+    // LDS buffer first, so those LDS writes overlap the MFMAs, and that register set is refilled
+    // with chunk kc+3; after the MFMAs the weight set is refilled with chunk kc+2.  One barrier
+    // per chunk orders both buffers.  KC is even (checked by the planner) and the body has no
+    // branches, so the accumulators stay in place; loads past the end re-read the last chunk into
+    // buffers nobody reads again.
+    for (int kc = 0; kc < KC; kc += 2) {
+        store_x(1, xr1);
+        load_x(kc + 3, xr1);
+        compute(0, w0, s0);
+        load_w(kc + 2, w0, s0);
+        __syncthreads();
+        store_x(0, xr0);
+        load_x(kc + 4, xr0);
+        compute(1, w1, s1);
+        load_w(kc + 3, w1, s1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        const int m = m0 + wm * WM + t * 16 + li;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = (nb0 + j) * 16 + 4 * kb;
+            if (m < M && nb0 + j < NBLK) *reinterpret_cast<u2*>(y + (size_t)m * N + n) = pack_f16x4(acc[t][j]);
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------ launch
 
 template <int CFG> struct PrefillCfg;
@@ -877,6 +1037,9 @@ W4A16_PREFILL_CFG(1)
 W4A16_PREFILL_CFG(2)
 W4A16_PREFILL_CFG(3)
 W4A16_PREFILL_CFG(4)
+W4A16_PREFILL_CFG(5)
+W4A16_PREFILL_CFG(6)
+W4A16_PREFILL_CFG(7)
 #undef W4A16_PREFILL_CFG
 
 template <int CFG>
@@ -885,8 +1048,12 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
     using C = PrefillCfg<CFG>;
     const int gshift = p.G == 128 ? 1 : 0;
     const int tiles_m = (p.M + C::BM - 1) / C::BM;
-    hipLaunchKernelGGL((prefill_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
-                       dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
+    if constexpr (kPrefillTable[CFG].wide)
+        hipLaunchKernelGGL((prefill_wide_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
+                           dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
+    else
+        hipLaunchKernelGGL((prefill_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
+                           dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
     return hipGetLastError();
 }
 
@@ -964,6 +1131,9 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
             case 2: e = launch_prefill<2>(p, wp, x, scales, y, st); break;
             case 3: e = launch_prefill<3>(p, wp, x, scales, y, st); break;
             case 4: e = launch_prefill<4>(p, wp, x, scales, y, st); break;
+            case 5: e = launch_prefill<5>(p, wp, x, scales, y, st); break;
+            case 6: e = launch_prefill<6>(p, wp, x, scales, y, st); break;
+            case 7: e = launch_prefill<7>(p, wp, x, scales, y, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }

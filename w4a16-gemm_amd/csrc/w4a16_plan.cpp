@@ -56,24 +56,37 @@ int prefill_occupancy(int cfg, const w4a16_device_limits& lim) {
     const int waves = kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n;
     occ = std::min(occ, 32 / waves);      // 8 wave slots per SIMD x 4 SIMDs
     occ = std::min(occ, 2);               // VGPR budget (acc + operands) of the larger tiles
-    return occ;
+    if (kPrefillTable[cfg].wide) occ = std::min(occ, std::max(1, 4 / waves));   // ~320 registers: 1 wave/SIMD
+    return std::max(occ, 0);
 }
 
 // Auto prefill selection (replaces pf_select, kernel.cu:142-156).  Cost = full-device waves of
-// tiles x per-wave work, where a tile's work is BN * (BM + 32): the MFMA work plus the
-// per-tile dequantisation overhead, which is paid once per weight column block and wave row.
-int prefill_select(int M, int N, const w4a16_device_limits& lim) {
+// tiles x per-wave work, where a tile's work is BN * (BM + D): the MFMA work plus the per-tile
+// dequantisation overhead D, paid once per weight column block and wave row (D = 32 rows for
+// prefill_kernel, 16 for the wide wave tiles whose dequantised operands feed twice as many
+// MFMAs).
+int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     int best = 0;
     double best_cost = std::numeric_limits<double>::infinity();
     const double cus = lim.cu_count > 0 ? lim.cu_count : 1;
-    for (int cfg = kNumPrefillCfg; cfg >= 1; --cfg) {      // descending: ties go to larger BM
+    // Large problems: the wide-tile kernels in the order measured fastest on MI355X (128 x 128
+    // tiles of 2 waves, then 128 x 256, then 256 x 128), when their tiles give every CU at least
+    // two rounds of full occupancy.
+    for (int cfg : {7, 5, 6}) {
         const int occ = prefill_occupancy(cfg, lim);
-        if (occ < 1) continue;
+        if (occ < 1 || !prefill_k_ok(cfg, K)) continue;
+        const PrefillTile& t = kPrefillTable[cfg];
+        const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
+        if (tiles >= 2.0 * cus * occ && tiles <= (double)std::numeric_limits<int32_t>::max()) return cfg;
+    }
+    for (int cfg = kNumPrefillTable; cfg >= 1; --cfg) {    // descending: ties go to the later config
+        const int occ = prefill_occupancy(cfg, lim);
+        if (occ < 1 || !prefill_k_ok(cfg, K)) continue;
         const PrefillTile& t = kPrefillTable[cfg];
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         if (tiles > (double)std::numeric_limits<int32_t>::max()) continue;
         const double waves = std::ceil(tiles / (cus * occ));
-        const double cost = waves * occ * t.bn * (t.bm + 32.0);
+        const double cost = waves * occ * t.bn * (t.bm + (t.wide ? 16.0 : 32.0));
         if (cost < best_cost) { best_cost = cost; best = cfg; }
     }
     return best;
@@ -208,8 +221,14 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
                          out.slab_chunks, splits, out.grid);
     } else {
         int cfg = v;                                          // 1..4 forced, or -1 = auto
-        if (cfg < 0) cfg = prefill_select(M, N, *lim);
-        if (!(cfg >= 1 && cfg <= kNumPrefillCfg && prefill_occupancy(cfg, *lim) > 0))
+        if (cfg < 0) {
+            if (const char* o = std::getenv("W4A16_PREFILL")) {   // tuning override: config id 1..7
+                const int oc = std::atoi(o);
+                if (oc >= 1 && oc <= kNumPrefillTable && prefill_occupancy(oc, *lim) > 0 && prefill_k_ok(oc, K)) cfg = oc;
+            }
+        }
+        if (cfg < 0) cfg = prefill_select(M, N, K, *lim);
+        if (!(cfg >= 1 && cfg <= kNumPrefillTable && prefill_occupancy(cfg, *lim) > 0))
             return fail(W4A16_ERR_NO_CONFIG, err, errlen,
                         "no prefill configuration fits (shared memory limit %d B, M=%d)", lim->lds_bytes_per_block, M);
         const PrefillTile& t = kPrefillTable[cfg];
