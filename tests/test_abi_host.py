@@ -166,7 +166,8 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
 
 
 @pytest.mark.parametrize("M,N,K,want", [
-    (2048, 28672, 8192, 7), (2048, 14336, 4096, 7), (4096, 4096, 4096, 7),   # wide tiles fill the device
+    (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
+    (2048, 14336, 4096, 7),                                                  # partial last round: 128x128
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
     (128, 14336, 4096, None)])                                               # too few wide tiles
 def test_prefill_wide_selection(lib, M, N, K, want):

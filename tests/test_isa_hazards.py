@@ -1,6 +1,6 @@
 """CPU check of the gfx950 assembly of the decode kernels (compiled here with hipcc -S).
 
-decode_lds_kernel, decode_stream_kernel and decode_ring_kernel issue some loads through inline asm (global_load_* into VGPRs, ds_read_b128)
+The decode LDS/stream/ring kernels and the wide prefill kernels issue loads through inline asm (global_load_* into VGPRs, ds_read_b128)
 so that the compiler's conservative waits do not serialise the weight stream.  The compiler does
 not know those registers are written asynchronously, so the kernel re-binds them after each
 explicit wait.  This test proves, for every instantiation, that no instruction reads or writes a
@@ -159,8 +159,9 @@ def _kernels(text):
 
 def test_untracked_load_registers_untouched_until_waited(isa):
     ks = _kernels(isa)
-    lds = [k for k in ks if "decode_lds_kernel" in k or "decode_stream_kernel" in k or "decode_ring_kernel" in k]
-    assert len(lds) >= 16 + 20, list(ks)
+    lds = [k for k in ks if any(n in k for n in ("decode_lds_kernel", "decode_stream_kernel", "decode_ring_kernel",
+                                                  "prefill_wide_kernel"))]
+    assert len(lds) >= 16 + 20 + 3, list(ks)
     problems = {k: check_kernel(ks[k]) for k in lds}
     bad = {k: v[:5] for k, v in problems.items() if v}
     assert not bad, bad

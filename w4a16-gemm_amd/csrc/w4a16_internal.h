@@ -7,10 +7,11 @@ namespace w4a16 {
 
 // Prefill tile configurations.  Ids 1..4 are the forced variants of the reference API (its
 // PfCfg<1..4>, src/vectorized/kernel.cu:59-63, re-tiled for 64-wide wavefronts and 256 CUs) and
-// run prefill_kernel; ids 5..7 run prefill_wide_kernel (wave tile 128 x 64) and are chosen by the
-// auto planner (or the W4A16_PREFILL override).  All give bit-identical output.
+// run prefill_kernel (kind 0); ids 5..7 run prefill_wide_kernel (kind 1, wave tile 128 x 64).
+// The auto planner (or the W4A16_PREFILL override) picks among all of them; all give
+// bit-identical output.
 struct PrefillTile {
-    int bm, bn, waves_m, waves_n, wide;
+    int bm, bn, waves_m, waves_n, kind;
 };
 constexpr PrefillTile kPrefillTable[8] = {
     {0, 0, 0, 0, 0},
@@ -29,8 +30,8 @@ constexpr int kNumPrefillTable = 7;      // all prefill configs
 constexpr int kLdsRowBytes = 144;
 
 constexpr int prefill_lds_bytes(int cfg) { return 2 * kPrefillTable[cfg].bm * kLdsRowBytes; }
-// The wide kernels walk K two chunks per iteration.
-constexpr bool prefill_k_ok(int cfg, int K) { return !kPrefillTable[cfg].wide || (K / 64) % 2 == 0; }
+// The wide kernels walk K two chunks per loop trip.
+constexpr bool prefill_k_ok(int cfg, int K) { return kPrefillTable[cfg].kind == 0 || (K / 64) % 2 == 0; }
 constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n; }
 
 // Decode kernel shapes.  A workgroup covers NBW n16 blocks (16*NBW output channels) with WAVES

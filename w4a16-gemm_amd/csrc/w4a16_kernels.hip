@@ -865,6 +865,18 @@ prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     }
 }
 
+// Untracked loads with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte offset.
+__device__ __forceinline__ u4 gload_u4_sbase(const void* base, uint32_t off) {
+    u4 v;
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(v) : "v"(off), "s"(base) : "memory");
+    return v;
+}
+__device__ __forceinline__ uint32_t gload_u16_sbase(const void* base, uint32_t off) {
+    uint32_t v;
+    asm volatile("global_load_ushort %0, %1, %2" : "=&v"(v) : "v"(off), "s"(base) : "memory");
+    return v;
+}
+
 // Prefill with large wave tiles (TM = WM/16 token blocks share each dequantised A operand).
 //
 // Same tile walk and MFMA order as prefill_kernel (every accumulator: chunk 0 h 0, chunk 0 h 1,
@@ -918,30 +930,36 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int nb0 = (n0 >> 4) + wn * TN;
     const int lanep = ((li & 7) << 2) | kb;
 
-    // Wave-uniform bases (SGPRs) plus 32-bit per-lane offsets keep the address registers few.
-    const u4* wbase[TN];
-    const uint16_t* sbase[TN];
+    // All global loads are issued through asm with a wave-uniform base (SGPRs, advanced per
+    // chunk) and a constant 32-bit per-lane byte offset, and waited for with explicit counts: the
+    // compiler's own wait placement drained every prefetch at the loop back-edge.
+    const char* wbase[TN];
+    const char* sbase[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int nbc = min(nb0 + j, NBLK - 1);
-        wbase[j] = Wp + (size_t)nbc * KC * 32;
-        sbase[j] = scales + (size_t)nbc * 16;
+        wbase[j] = reinterpret_cast<const char*>(Wp + (size_t)nbc * KC * 32);
+        sbase[j] = reinterpret_cast<const char*>(scales + (size_t)nbc * 16);
     }
-    const uint16_t* xbase = x + (size_t)m0 * K;
-    uint32_t xoff[SPT];                                        // halves, relative to row m0
+    const uint32_t woff = (uint32_t)lanep * 16;
+    const uint32_t soff = (uint32_t)li * 2;
+    const char* xbase = reinterpret_cast<const char*>(x + (size_t)m0 * K);
+    uint32_t xoff[SPT];                                        // bytes, relative to row m0, chunk 0
 #pragma unroll
     for (int r = 0; r < SPT; ++r) {
         const int sg = tid + r * NT;
-        xoff[r] = (uint32_t)(min(m0 + (sg >> 3), M - 1) - m0) * (uint32_t)K + (sg & 7) * 8;
+        xoff[r] = ((uint32_t)(min(m0 + (sg >> 3), M - 1) - m0) * (uint32_t)K + (sg & 7) * 8) * 2;
     }
 
     u4 xr0[SPT], xr1[SPT];
     auto load_x = [&](int kc, u4 (&xr)[SPT]) {
-        const uint32_t kcl = (uint32_t)min(kc, KC - 1);       // past the end: harmless reload
+        const char* xb = xbase + (size_t)min(kc, KC - 1) * 128;   // past the end: harmless reload
 #pragma unroll
-        for (int r = 0; r < SPT; ++r) xr[r] = *reinterpret_cast<const u4*>(xbase + xoff[r] + kcl * 64);
+        for (int r = 0; r < SPT; ++r) xr[r] = gload_u4_sbase(xb, xoff[r]);
     };
-    auto store_x = [&](int buf, const u4 (&xr)[SPT]) {
+    auto store_x = [&](int buf, u4 (&xr)[SPT]) {
+#pragma unroll
+        for (int r = 0; r < SPT; ++r) bind_after_wait(xr[r]);
 #pragma unroll
         for (int r = 0; r < SPT; ++r) {
             const int sg = tid + r * NT;
@@ -949,15 +967,20 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         }
     };
     u4 w0[TN], w1[TN];
-    uint16_t s0[TN], s1[TN];
-    auto load_w = [&](int kc, u4 (&w)[TN], uint16_t (&s)[TN]) {
-        const int kcl = min(kc, KC - 1);                     // past the end: harmless reload
+    uint32_t s0[TN], s1[TN];
+    auto load_w = [&](int kc, u4 (&w)[TN], uint32_t (&s)[TN]) {
+        const int kcl = min(kc, KC - 1);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            w[j] = wbase[j][(uint32_t)kcl * 32 + lanep];
-            s[j] = sbase[j][(uint32_t)(kcl >> gshift) * (uint32_t)N + li];
-        }
+        for (int j = 0; j < TN; ++j) w[j] = gload_u4_sbase(wbase[j] + (size_t)kcl * 512, woff);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) s[j] = gload_u16_sbase(sbase[j] + (size_t)(kcl >> gshift) * N * 2, soff);
     };
+    // Loads younger than x of chunk c+1 when chunk c starts (weights c, x c+2, weights c+1), and
+    // younger than the weights of chunk c once x of chunk c+3 is issued (x c+2, weights c+1,
+    // x c+3): see the issue order below.
+    constexpr int WAIT_X = 4 * TN + SPT;
+    constexpr int WAIT_W = 2 * SPT + 2 * TN;
+    static_assert(WAIT_X <= 63 && WAIT_W <= 63, "vmcnt range");
 
     f4 acc[TM][TN];
 #pragma unroll
@@ -969,7 +992,9 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const char* xrow = xs + (wm * WM + li) * kXRow + kb * 16;
     // One chunk: for each half h, all TM B operands are read from LDS first (one wait, not one
     // per token block), the TN A operands are dequantised, then the TM x TN MFMAs run.
-    auto compute = [&](int buf, const u4 (&w)[TN], const uint16_t (&s)[TN]) {
+    auto compute = [&](int buf, u4 (&w)[TN], uint32_t (&s)[TN]) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) { bind_after_wait(w[j]); bind_after_wait(s[j]); }
         const char* xb = xrow + buf * XBUF;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -978,8 +1003,10 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             for (int t = 0; t < TM; ++t) bf[t] = *reinterpret_cast<const h8*>(xb + t * 16 * kXRow + h * 64);
             h8 a[TN];
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                a[j] = h ? dq_frag(w[j].z, w[j].w, d, scale2(s[j])) : dq_frag(w[j].x, w[j].y, d, scale2(s[j]));
+            for (int j = 0; j < TN; ++j) {
+                const h2 s2 = scale2((uint16_t)s[j]);
+                a[j] = h ? dq_frag(w[j].z, w[j].w, d, s2) : dq_frag(w[j].x, w[j].y, d, s2);
+            }
 #pragma unroll
             for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -987,31 +1014,43 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         }
     };
 
+    // Issue order: prologue x0 | x1 w0 x2 w1; then chunk c issues x(c+3) and w(c+2).  Chunk c
+    // uses x buffer c & 1, x register set and weight set c & 1 (the loop is unrolled by two
+    // chunks; K/64 is even, checked by the planner).  x of chunk c+1 is written to the other LDS
+    // buffer first, so those LDS writes overlap the MFMAs.  One barrier per chunk orders both
+    // buffers.  Loads past the end re-read the last chunk into registers nobody uses again.
     load_x(0, xr0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    store_x(0, xr0);
     load_x(1, xr1);
     load_w(0, w0, s0);
-    load_w(1, w1, s1);
-    store_x(0, xr0);
     load_x(2, xr0);
+    load_w(1, w1, s1);
     __syncthreads();
-    // Two chunks per loop trip.  Chunk kc: its x is in LDS buffer kc & 1 and its weights in
-    // register set kc & 1; x of chunk kc+1 (in the other x register set) is written to the other
-    // LDS buffer first, so those LDS writes overlap the MFMAs, and that register set is refilled
-    // with chunk kc+3; after the MFMAs the weight set is refilled with chunk kc+2.  One barrier
-    // per chunk orders both buffers.  KC is even (checked by the planner) and the body has no
-    // branches, so the accumulators stay in place; loads past the end re-read the last chunk into
-    // buffers nobody reads again.
     for (int kc = 0; kc < KC; kc += 2) {
+        wait_vmcnt(WAIT_X);
         store_x(1, xr1);
         load_x(kc + 3, xr1);
+        wait_vmcnt(WAIT_W);
         compute(0, w0, s0);
         load_w(kc + 2, w0, s0);
         __syncthreads();
+        wait_vmcnt(WAIT_X);
         store_x(0, xr0);
         load_x(kc + 4, xr0);
+        wait_vmcnt(WAIT_W);
         compute(1, w1, s1);
         load_w(kc + 3, w1, s1);
         __syncthreads();
+    }
+    // No load in flight at exit.  The registers of the last (unused) prefetches are re-bound
+    // after the wait: otherwise the compiler, seeing them dead, reuses them before it.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < SPT; ++r) { bind_after_wait(xr0[r]); bind_after_wait(xr1[r]); }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        bind_after_wait(w0[j]); bind_after_wait(s0[j]); bind_after_wait(w1[j]); bind_after_wait(s1[j]);
     }
 
 #pragma unroll
@@ -1048,7 +1087,7 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
     using C = PrefillCfg<CFG>;
     const int gshift = p.G == 128 ? 1 : 0;
     const int tiles_m = (p.M + C::BM - 1) / C::BM;
-    if constexpr (kPrefillTable[CFG].wide)
+    if constexpr (kPrefillTable[CFG].kind == 1)
         hipLaunchKernelGGL((prefill_wide_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
                            dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
     else

@@ -56,7 +56,7 @@ int prefill_occupancy(int cfg, const w4a16_device_limits& lim) {
     const int waves = kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n;
     occ = std::min(occ, 32 / waves);      // 8 wave slots per SIMD x 4 SIMDs
     occ = std::min(occ, 2);               // VGPR budget (acc + operands) of the larger tiles
-    if (kPrefillTable[cfg].wide) occ = std::min(occ, std::max(1, 4 / waves));   // ~320 registers: 1 wave/SIMD
+    if (kPrefillTable[cfg].kind == 1) occ = std::min(occ, std::max(1, 4 / waves));   // ~320 registers: 1 wave/SIMD
     return std::max(occ, 0);
 }
 
@@ -69,15 +69,23 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     int best = 0;
     double best_cost = std::numeric_limits<double>::infinity();
     const double cus = lim.cu_count > 0 ? lim.cu_count : 1;
-    // Large problems: the wide-tile kernels in the order measured fastest on MI355X (128 x 128
-    // tiles of 2 waves, then 128 x 256, then 256 x 128), when their tiles give every CU at least
-    // two rounds of full occupancy.
-    for (int cfg : {7, 5, 6}) {
-        const int occ = prefill_occupancy(cfg, lim);
-        if (occ < 1 || !prefill_k_ok(cfg, K)) continue;
+    // Large problems: the wide-tile kernels, when their tiles give every CU at least two rounds
+    // of full occupancy, in the order measured fastest on MI355X: 128 x 256 tiles (one workgroup
+    // per CU) when they fill whole rounds exactly, else 128 x 128 tiles of 2 waves (two per CU,
+    // shorter tails), then 128 x 256, then 256 x 128.
+    auto wide_tiles = [&](int cfg, int& occ) {
+        occ = prefill_occupancy(cfg, lim);
+        if (occ < 1 || !prefill_k_ok(cfg, K)) return -1.0;
         const PrefillTile& t = kPrefillTable[cfg];
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
-        if (tiles >= 2.0 * cus * occ && tiles <= (double)std::numeric_limits<int32_t>::max()) return cfg;
+        return tiles >= 2.0 * cus * occ && tiles <= (double)std::numeric_limits<int32_t>::max() ? tiles : -1.0;
+    };
+    int occ5 = 0;
+    const double t5 = wide_tiles(5, occ5);
+    if (t5 > 0 && std::fmod(t5, cus * occ5) == 0.0) return 5;
+    for (int cfg : {7, 5, 6}) {
+        int occ = 0;
+        if (wide_tiles(cfg, occ) > 0) return cfg;
     }
     for (int cfg = kNumPrefillTable; cfg >= 1; --cfg) {    // descending: ties go to the later config
         const int occ = prefill_occupancy(cfg, lim);
@@ -86,7 +94,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         if (tiles > (double)std::numeric_limits<int32_t>::max()) continue;
         const double waves = std::ceil(tiles / (cus * occ));
-        const double cost = waves * occ * t.bn * (t.bm + (t.wide ? 16.0 : 32.0));
+        const double cost = waves * occ * t.bn * (t.bm + (t.kind ? 16.0 : 32.0));
         if (cost < best_cost) { best_cost = cost; best = cfg; }
     }
     return best;
