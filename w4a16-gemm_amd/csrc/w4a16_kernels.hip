@@ -989,28 +989,34 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         for (int j = 0; j < TN; ++j) acc[t][j] = f4{0.f, 0.f, 0.f, 0.f};
 
     const Dq d = dq_setup(lane);
-    const char* xrow = xs + (wm * WM + li) * kXRow + kb * 16;
-    // One chunk: for each half h, all TM B operands are read from LDS first (one wait, not one
-    // per token block), the TN A operands are dequantised, then the TM x TN MFMAs run.
+    const uint32_t xrow = (uint32_t)reinterpret_cast<uintptr_t>(xs) + (wm * WM + li) * kXRow + kb * 16;
+    // One chunk: for each half h, all TM B operands are read from LDS through asm (the compiler
+    // would interleave each read with a full lgkmcnt wait), the TN A operands are dequantised
+    // while the reads are in flight, then one wait and the TM x TN MFMAs.
     auto compute = [&](int buf, u4 (&w)[TN], uint32_t (&s)[TN]) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) { bind_after_wait(w[j]); bind_after_wait(s[j]); }
-        const char* xb = xrow + buf * XBUF;
+        const uint32_t xb = xrow + buf * XBUF;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            h8 bf[TM];
+            u4 bv[TM];
 #pragma unroll
-            for (int t = 0; t < TM; ++t) bf[t] = *reinterpret_cast<const h8*>(xb + t * 16 * kXRow + h * 64);
+            for (int t = 0; t < TM; ++t) bv[t] = lds_read_u4(xb + t * 16 * kXRow + h * 64);
             h8 a[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const h2 s2 = scale2((uint16_t)s[j]);
                 a[j] = h ? dq_frag(w[j].z, w[j].w, d, s2) : dq_frag(w[j].x, w[j].y, d, s2);
             }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-            for (int t = 0; t < TM; ++t)
+            for (int t = 0; t < TM; ++t) bind_after_wait(bv[t]);
 #pragma unroll
-                for (int j = 0; j < TN; ++j) acc[t][j] = mfma16x16x32(a[j], bf[t], acc[t][j]);
+            for (int t = 0; t < TM; ++t) {
+                const h8 bf = __builtin_bit_cast(h8, bv[t]);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[t][j] = mfma16x16x32(a[j], bf, acc[t][j]);
+            }
         }
     };
 
