@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 7
+        assert 1 <= p.kernel <= 9
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -162,14 +162,18 @@ def test_prefill_plan_invariants(lib, M, N):
     assert p.workspace_bytes == 0 and p.counter_slots == 0
 
 
-PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128)}
+PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128),
+                 8: (32, 16), 9: (64, 16)}
 
 
 @pytest.mark.parametrize("M,N,K,want", [
     (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
     (2048, 14336, 4096, 7),                                                  # partial last round: 128x128
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
-    (128, 14336, 4096, None)])                                               # too few wide tiles
+    (128, 14336, 4096, None),                                                # too few wide tiles
+    (17, 4096, 14336, 8), (32, 14336, 4096, 8), (33, 4096, 4096, 9), (64, 4096, 4096, 9),  # few token rows
+    (48, 14336, 4096, None),                                                 # many blocks: 16 x 128 tiles
+    (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
     assert rc == 0, err
@@ -179,7 +183,7 @@ def test_prefill_wide_selection(lib, M, N, K, want):
         assert p.kernel == want
     tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
-    assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2}[p.kernel]
+    assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1}[p.kernel]
 
 
 def test_prefill_override(lib, monkeypatch):
@@ -190,6 +194,11 @@ def test_prefill_override(lib, monkeypatch):
     monkeypatch.setenv("W4A16_PREFILL", "5")                  # wide config, odd chunk count: ignored
     rc, p, err = plan(lib, M=2048, N=4096, K=4160, G=64)
     assert rc == 0 and 1 <= p.kernel <= 4
+    monkeypatch.setenv("W4A16_PREFILL", "8")                  # small-M config: only when M fits
+    rc, p, err = plan(lib, M=40, N=4096, K=4096, G=128)
+    assert rc == 0 and p.kernel != 8
+    rc, p, err = plan(lib, M=20, N=4096, K=4096, G=128)
+    assert rc == 0 and p.kernel == 8 and p.grid == 4096 // 16 and p.block == 64
     monkeypatch.setenv("W4A16_PREFILL", "3")                  # a forced variant wins over the override
     rc, p, err = plan(lib, M=2048, N=4096, K=4096, G=128, variant=2)
     assert rc == 0 and p.kernel == 2

@@ -433,3 +433,21 @@ def test_prefill_wide_configs_bitwise_equal(cfg, M, N, K, G, monkeypatch):
     assert torch.equal(y, gemm(Wp, x, scales, variant=1))
     assert_close(y, ref_gemm(x, q, scales, G, key))
     assert torch.equal(gemm(Wp, x[:M // 2 + 1].contiguous(), scales), y[:M // 2 + 1])
+
+
+# Small-M prefill (M = 17..64, chosen automatically): one wave per n16 block over the whole K,
+# bit-identical to the reference-API variants.
+@pytest.mark.parametrize("M,N,K,G", [(17, 4096, 4096, 128), (32, 1040, 2048, 64), (33, 256, 1024, 128),
+                                     (64, 272, 1024, 64), (20, 16, 1024, 64), (40, 512, 14336, 128)])
+def test_prefill_small_m_bitwise_equal(M, N, K, G):
+    torch = torch_cuda()
+    import w4a16_opt
+    assert "prefill_stream_kernel" in w4a16_opt.plan_info(M, N, K, G)["kernel_name"]
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=M)
+    y = gemm(Wp, x, scales)
+    assert torch.equal(y, gemm(Wp, x, scales, variant=4))
+    assert torch.equal(y, gemm(Wp, x, scales, variant=1))
+    assert_close(y, ref_gemm(x, q, scales, G, key))
+    for m in (17, M - 1):
+        if 17 <= m < M:
+            assert torch.equal(gemm(Wp, x[:m].contiguous(), scales), y[:m]), m

@@ -7,31 +7,43 @@ namespace w4a16 {
 
 // Prefill tile configurations.  Ids 1..4 are the forced variants of the reference API (its
 // PfCfg<1..4>, src/vectorized/kernel.cu:59-63, re-tiled for 64-wide wavefronts and 256 CUs) and
-// run prefill_kernel (kind 0); ids 5..7 run prefill_wide_kernel (kind 1, wave tile 128 x 64).
-// The auto planner (or the W4A16_PREFILL override) picks among all of them; all give
-// bit-identical output.
+// run prefill_kernel (kind 0); ids 5..7 run prefill_wide_kernel (kind 1, wave tile 128 x 64);
+// ids 8..9 run prefill_stream_kernel (kind 2: one wave per n16 block over the whole K, for
+// M <= bm, ring of `depth` chunk pairs).  The auto planner (or the W4A16_PREFILL override)
+// picks among all of them; all give bit-identical output.
 struct PrefillTile {
-    int bm, bn, waves_m, waves_n, kind;
+    int bm, bn, waves_m, waves_n, kind, depth;
 };
-constexpr PrefillTile kPrefillTable[8] = {
-    {0, 0, 0, 0, 0},
-    {16, 128, 1, 4, 0},     // 1: small batches: 4 waves across N, wave tile 16 x 32
-    {32, 128, 1, 4, 0},     // 2: wave tile 32 x 32
-    {64, 128, 2, 2, 0},     // 3: wave tile 32 x 64
-    {128, 128, 2, 2, 0},    // 4: wave tile 64 x 64
-    {128, 256, 1, 4, 1},    // 5: wave tile 128 x 64, 4 waves across N
-    {256, 128, 2, 2, 1},    // 6: wave tile 128 x 64, 2 x 2 waves
-    {128, 128, 1, 2, 1},    // 7: wave tile 128 x 64, 2 waves
+constexpr PrefillTile kPrefillTable[10] = {
+    {0, 0, 0, 0, 0, 0},
+    {16, 128, 1, 4, 0, 0},     // 1: small batches: 4 waves across N, wave tile 16 x 32
+    {32, 128, 1, 4, 0, 0},     // 2: wave tile 32 x 32
+    {64, 128, 2, 2, 0, 0},     // 3: wave tile 32 x 64
+    {128, 128, 2, 2, 0, 0},    // 4: wave tile 64 x 64
+    {128, 256, 1, 4, 1, 0},    // 5: wave tile 128 x 64, 4 waves across N
+    {256, 128, 2, 2, 1, 0},    // 6: wave tile 128 x 64, 2 x 2 waves
+    {128, 128, 1, 2, 1, 0},    // 7: wave tile 128 x 64, 2 waves
+    {32, 16, 1, 1, 2, 6},      // 8: M <= 32, one wave per n16 block, 6 pairs in flight
+    {64, 16, 1, 1, 2, 3},      // 9: M <= 64, one wave per n16 block, 3 pairs in flight
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 7;      // all prefill configs
+constexpr int kNumPrefillTable = 9;      // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;
 
-constexpr int prefill_lds_bytes(int cfg) { return 2 * kPrefillTable[cfg].bm * kLdsRowBytes; }
-// The wide kernels walk K two chunks per loop trip.
-constexpr bool prefill_k_ok(int cfg, int K) { return kPrefillTable[cfg].kind == 0 || (K / 64) % 2 == 0; }
+constexpr int prefill_lds_bytes(int cfg) {
+    return kPrefillTable[cfg].kind == 2
+               ? (kPrefillTable[cfg].depth + 1) * (2048 + kPrefillTable[cfg].bm / 4 * 1024)   // ring slots
+               : 2 * kPrefillTable[cfg].bm * kLdsRowBytes;
+}
+// Kinds 1 and 2 walk K two chunks at a time; kind 2 covers all M in one tile and needs at least
+// `depth` chunk pairs.
+constexpr bool prefill_shape_ok(int cfg, int M, int K) {
+    return kPrefillTable[cfg].kind == 0 ||
+           ((K / 64) % 2 == 0 &&
+            (kPrefillTable[cfg].kind != 2 || (M <= kPrefillTable[cfg].bm && K / 128 >= kPrefillTable[cfg].depth)));
+}
 constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n; }
 
 // Decode kernel shapes.  A workgroup covers NBW n16 blocks (16*NBW output channels) with WAVES

@@ -1070,6 +1070,144 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     }
 }
 
+// Small-M prefill (17 <= M <= 16*TM): one wave per n16 block walks the whole K range.
+//
+// With few token rows the prefill tiles leave most CUs idle (N/BN workgroups) and a K-sequential
+// wave is latency-bound.  Here every n16 block gets its own wave (N/16 workgroups of one wave)
+// that streams its weights through a refill-ahead ring of D+1 chunk-pair slots in LDS (the
+// decode_ring_kernel scheme): the loads of pair p+D are issued before pair p is multiplied.  A
+// slot holds the block's two 512-byte weight chunks (segments transposed for conflict-free A
+// reads) and the pair's 16*TM x rows (16-byte segments XOR-swizzled by row); the pair's scales
+// come straight into VGPRs.  Every accumulator receives chunk 0 h 0, chunk 0 h 1, chunk 1 h 0,
+// ... with the same A (dq_frag) and B operands (8 consecutive halves, row-transposed), so the
+// output is bit-identical to every other prefill config.  All loads run with all lanes active
+// (clamped addresses), so each pair is exactly OPS vector-memory instructions.
+template <int TM, int D>
+__global__ void __launch_bounds__(64)
+prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
+                      const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
+                      int M, int N, int K, int gshift) {
+    constexpr int S = D + 1;                                 // ring slots
+    constexpr int XD = 4 * TM;                               // x loads per pair (4 rows each)
+    constexpr int SLOT = 1024 + XD * 1024 + 1024;            // weights, 16*TM rows x 256 B, scales
+    constexpr int SOFF = 1024 + XD * 1024;                   // scale region of a slot
+    constexpr int OPS = 1 + XD + 1;                          // weights, x rows, scales
+    static_assert((D - 1) * OPS <= 63, "too many loads in flight for vmcnt");
+    __shared__ __attribute__((aligned(16))) char wl[S * SLOT];
+
+    const int lane = threadIdx.x;
+    const int kb = lane >> 4;
+    const int li = lane & 15;
+    const int nb = blockIdx.x;
+    const int KC = K >> 6;
+    const int npair = KC >> 1;
+    const uint32_t lds = (uint32_t)reinterpret_cast<uintptr_t>(wl);
+
+    // Weights: lane j fills segment j & 31 of chunk j >> 5 with packed lane 4*(seg % 8) + seg / 8.
+    const int wseg = lane & 31;
+    const u4* wsrc = Wp + ((size_t)nb * KC + (lane >> 5)) * 32 + 4 * (wseg & 7) + (wseg >> 3);
+    // x: lane j of load q fills row r = (64q + j) / 16, segment j % 16, with global segment
+    // (j % 16) ^ (r % 8) of row min(r, M - 1).
+    const uint16_t* xsrc[XD];
+#pragma unroll
+    for (int q = 0; q < XD; ++q) {
+        const int r = (64 * q + lane) >> 4;
+        xsrc[q] = x + (size_t)min(r, M - 1) * K + (((lane & 15) ^ (r & 7)) * 8);
+    }
+    // Scales: the pair's 2 chunks x 16 channels are 4 16-byte pieces (chunk c = (j >> 1) & 1,
+    // channels 8*(j & 1)..+7); lane j loads piece j & 3, so the other lanes repeat them.
+    const uint16_t* ssrc = scales + (size_t)nb * 16 + (lane & 1) * 8;
+    const int scc = (lane >> 1) & 1;
+    auto issue = [&](int p, int s) {
+        char* sl = wl + s * SLOT;
+        __builtin_amdgcn_global_load_lds((const void*)(wsrc + (size_t)p * 64),
+                                         (__attribute__((address_space(3))) void*)sl, 16, 0, 0);
+#pragma unroll
+        for (int q = 0; q < XD; ++q)
+            __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * 128),
+                                             (__attribute__((address_space(3))) void*)(sl + 1024 + q * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)((2 * p + scc) >> gshift) * N),
+                                         (__attribute__((address_space(3))) void*)(sl + SOFF), 16, 0, 0);
+        asm volatile("" ::: "memory");
+    };
+
+    uint32_t xoff[TM][2][2];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        const int r = min(16 * t + li, M - 1);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) xoff[t][cc][h] = 1024 + r * 256 + (((cc * 8 + 4 * h + kb) ^ (r & 7)) << 4);
+    }
+    const uint32_t woff = ((li & 7) + 8 * kb) << 4;
+    const uint32_t soff = SOFF + (li >> 3) * 16 + (li & 7) * 2;     // + 32 * chunk
+    const Dq d = dq_setup(lane);
+    f4 acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+
+    auto consume = [&](int s) {
+        const uint32_t base = lds + s * SLOT;
+        u4 wv[2], xv[TM][2][2];
+        uint32_t sv[2];
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) wv[cc] = lds_read_u4(base + cc * 512 + woff);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) sv[cc] = lds_read_u16(base + soff + cc * 32);
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) xv[t][cc][h] = lds_read_u4(base + xoff[t][cc][h]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            bind_after_wait(wv[cc]);
+            bind_after_wait(sv[cc]);
+#pragma unroll
+            for (int t = 0; t < TM; ++t) { bind_after_wait(xv[t][cc][0]); bind_after_wait(xv[t][cc][1]); }
+        }
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const h2 s2 = scale2((uint16_t)sv[cc]);
+            const h8 a0 = dq_frag(wv[cc].x, wv[cc].y, d, s2);
+            const h8 a1 = dq_frag(wv[cc].z, wv[cc].w, d, s2);
+#pragma unroll
+            for (int t = 0; t < TM; ++t) acc[t] = mfma16x16x32(a0, __builtin_bit_cast(h8, xpose_rows(xv[t][cc][0])), acc[t]);
+#pragma unroll
+            for (int t = 0; t < TM; ++t) acc[t] = mfma16x16x32(a1, __builtin_bit_cast(h8, xpose_rows(xv[t][cc][1])), acc[t]);
+        }
+    };
+
+    // Prologue: pairs 0..D-1 (npair >= D, checked by the planner).  Steady state: wait for pair
+    // p, refill with pair p + D, then compute pair p.  Drain: the last D pairs.
+#pragma unroll
+    for (int s = 0; s < D; ++s) issue(s, s);
+    int sc = 0, si = D;
+    int p = 0;
+    for (; p + D < npair; ++p) {
+        wait_vmcnt((D - 1) * OPS);
+        issue(p + D, si);
+        consume(sc);
+        sc = sc + 1 == S ? 0 : sc + 1;
+        si = si + 1 == S ? 0 : si + 1;
+    }
+#pragma unroll
+    for (int t = 0; t < D; ++t) {
+        wait_vmcnt((D - 1 - t) * OPS);
+        consume(sc);
+        sc = sc + 1 == S ? 0 : sc + 1;
+    }
+
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        const int m = 16 * t + li;
+        if (m < M) *reinterpret_cast<u2*>(y + (size_t)m * N + nb * 16 + 4 * kb) = pack_f16x4(acc[t]);
+    }
+}
+
 // ------------------------------------------------------------------------------------ launch
 
 template <int CFG> struct PrefillCfg;
@@ -1085,6 +1223,8 @@ W4A16_PREFILL_CFG(4)
 W4A16_PREFILL_CFG(5)
 W4A16_PREFILL_CFG(6)
 W4A16_PREFILL_CFG(7)
+W4A16_PREFILL_CFG(8)
+W4A16_PREFILL_CFG(9)
 #undef W4A16_PREFILL_CFG
 
 template <int CFG>
@@ -1093,7 +1233,10 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
     using C = PrefillCfg<CFG>;
     const int gshift = p.G == 128 ? 1 : 0;
     const int tiles_m = (p.M + C::BM - 1) / C::BM;
-    if constexpr (kPrefillTable[CFG].kind == 1)
+    if constexpr (kPrefillTable[CFG].kind == 2)
+        hipLaunchKernelGGL((prefill_stream_kernel<C::BM / 16, kPrefillTable[CFG].depth>), dim3(p.grid), dim3(64), 0, st,
+                           Wp, x, s, y, p.M, p.N, p.K, gshift);
+    else if constexpr (kPrefillTable[CFG].kind == 1)
         hipLaunchKernelGGL((prefill_wide_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
                            dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
     else
@@ -1179,6 +1322,8 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
             case 5: e = launch_prefill<5>(p, wp, x, scales, y, st); break;
             case 6: e = launch_prefill<6>(p, wp, x, scales, y, st); break;
             case 7: e = launch_prefill<7>(p, wp, x, scales, y, st); break;
+            case 8: e = launch_prefill<8>(p, wp, x, scales, y, st); break;
+            case 9: e = launch_prefill<9>(p, wp, x, scales, y, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }

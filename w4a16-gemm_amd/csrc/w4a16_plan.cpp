@@ -75,11 +75,17 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     // shorter tails), then 128 x 256, then 256 x 128.
     auto wide_tiles = [&](int cfg, int& occ) {
         occ = prefill_occupancy(cfg, lim);
-        if (occ < 1 || !prefill_k_ok(cfg, K)) return -1.0;
+        if (occ < 1 || !prefill_shape_ok(cfg, M, K)) return -1.0;
         const PrefillTile& t = kPrefillTable[cfg];
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         return tiles >= 2.0 * cus * occ && tiles <= (double)std::numeric_limits<int32_t>::max() ? tiles : -1.0;
     };
+    // Few token rows: one wave per n16 block over the whole K (prefill_stream_kernel) instead of
+    // tiles that leave most CUs idle.  Measured on MI355X: faster for every N at M <= 32 (e.g.
+    // K = 14336, N = 4096: 53 vs 154 us), and at M <= 64 when N/16 blocks are at most twice the
+    // CU count (at N = 14336, M = 48 the 16 x 128 tiles win).
+    if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K)) return 8;
+    if (prefill_occupancy(9, lim) > 0 && prefill_shape_ok(9, M, K) && N / 16 <= 2 * lim.cu_count) return 9;
     int occ5 = 0;
     const double t5 = wide_tiles(5, occ5);
     if (t5 > 0 && std::fmod(t5, cus * occ5) == 0.0) return 5;
@@ -89,7 +95,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     }
     for (int cfg = kNumPrefillTable; cfg >= 1; --cfg) {    // descending: ties go to the later config
         const int occ = prefill_occupancy(cfg, lim);
-        if (occ < 1 || !prefill_k_ok(cfg, K)) continue;
+        if (occ < 1 || !prefill_shape_ok(cfg, M, K)) continue;
         const PrefillTile& t = kPrefillTable[cfg];
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         if (tiles > (double)std::numeric_limits<int32_t>::max()) continue;
@@ -230,9 +236,9 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
     } else {
         int cfg = v;                                          // 1..4 forced, or -1 = auto
         if (cfg < 0) {
-            if (const char* o = std::getenv("W4A16_PREFILL")) {   // tuning override: config id 1..7
+            if (const char* o = std::getenv("W4A16_PREFILL")) {   // tuning override: config id 1..9
                 const int oc = std::atoi(o);
-                if (oc >= 1 && oc <= kNumPrefillTable && prefill_occupancy(oc, *lim) > 0 && prefill_k_ok(oc, K)) cfg = oc;
+                if (oc >= 1 && oc <= kNumPrefillTable && prefill_occupancy(oc, *lim) > 0 && prefill_shape_ok(oc, M, K)) cfg = oc;
             }
         }
         if (cfg < 0) cfg = prefill_select(M, N, K, *lim);
