@@ -95,7 +95,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     }
     for (int cfg = kNumPrefillTable; cfg >= 1; --cfg) {    // descending: ties go to the later config
         const int occ = prefill_occupancy(cfg, lim);
-        if (occ < 1 || !prefill_shape_ok(cfg, M, K)) continue;
+        if (occ < 1 || !prefill_shape_ok(cfg, M, K) || kPrefillTable[cfg].kind == 2) continue;   // kind 2: rule above
         const PrefillTile& t = kPrefillTable[cfg];
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         if (tiles > (double)std::numeric_limits<int32_t>::max()) continue;
