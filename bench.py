@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X W4A16 GEMM on BASELINE.json's metric.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill|quantize]
                     [--no-cpu] [--no-prefill] [--json PATH]
 
 Headline (default): decode GB/s on the Llama-3-8B MLP shapes,
@@ -164,6 +164,54 @@ def bench_copy(torch, steps):
             "launches": steps}
 
 
+QUANT_CASE = ("mlp70b", 28672, 8192)
+
+
+def quant_bytes(N, K, G=G):
+    """Algorithmic bytes of one quantise+pack of an fp16 [N, K] weight: read W, write Wp and scales."""
+    return N * K * 2 + N * K // 2 + (K // G) * N * 2
+
+
+def bench_quantize(torch, steps, warmup):
+    """Device quantise + pack (w4a16_opt.quantize_pack) of the BASELINE prefill weight, fp16 input.
+    W (470 MB) exceeds the Infinity Cache, so every launch streams it from HBM."""
+    import w4a16_opt
+    name, N, K = QUANT_CASE
+    W = (torch.randn(N, K, device="cuda") * 0.02).half()
+    for _ in range(max(1, warmup)):
+        w4a16_opt.quantize_pack(W, G)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        w4a16_opt.quantize_pack(W, G)
+    end.record()
+    end.synchronize()
+    us = start.elapsed_time(end) * 1e3 / steps
+    gbs = quant_bytes(N, K) / (us * 1e-6) / 1e9
+    log(f"quantize_pack {name} N={N} K={K}: {us:.1f} us  {gbs:.1f} GB/s")
+    return {"us": us, "GBs": gbs}
+
+
+def cpu_baseline_quantize(max_seconds=12.0):
+    """The oracle's numpy quantize_w4 + pack_int4 (restatement of the reference's torch CPU path)
+    on 1024-row slices of the quantise workload until max_seconds (rate is size-independent)."""
+    import numpy as np
+    from oracle import quant
+    _, N, K = QUANT_CASE
+    R = 1024
+    W = (np.random.default_rng(12).standard_normal((R, K), dtype=np.float32) * np.float32(0.02)).astype(np.float16)
+    done, dt = 0, 0.0
+    while dt < max_seconds and done < N // R:
+        t0 = time.perf_counter()
+        q, _ = quant.quantize_w4(W.astype(np.float32), G)
+        quant.pack_int4(q)
+        dt += time.perf_counter() - t0
+        done += 1
+    return {"value": round(quant_bytes(done * R, K) / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle numpy quantize_w4 + pack_int4 on {done} slices of 1024 x {K} fp16 ({dt:.2f} s)"}
+
+
 def cpu_baseline(cases, max_seconds=20.0):
     """Time the oracle's C restatement of the reference CPU path on the host (bounded sample)."""
     import numpy as np
@@ -222,8 +270,9 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--workload", choices=("decode", "prefill", "copy"), default="decode",
-                    help="copy: HBM-counter calibration kernel (64 MiB elementwise copy), no benchmark line")
+    ap.add_argument("--workload", choices=("decode", "prefill", "quantize", "copy"), default="decode",
+                    help="quantize: device quantise+pack of the prefill weight; "
+                         "copy: HBM-counter calibration kernel (64 MiB elementwise copy), no benchmark line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--json", default=None, help="also write the JSON line to this file")
@@ -244,6 +293,25 @@ def main(argv=None) -> int:
 
     if a.workload == "copy":
         print(json.dumps(bench_copy(torch, a.steps)), flush=True)
+        return 0
+    if a.workload == "quantize":
+        qr = bench_quantize(torch, a.steps, a.warmup)
+        _, N, K = QUANT_CASE
+        out = {"metric": "quantize+pack GB/s (algorithmic bytes: fp16 W read, Wp + scales written)",
+               "value": round(qr["GBs"], 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+               "ms_per_step": round(qr["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+               "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+               "config": {"workload": f"quantize_pack of an fp16 [{N}, {K}] weight (BASELINE configs[3] weight), G={G}"},
+               "roofline": {"bound": "hbm", "achieved": round(qr["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(qr["GBs"] / HBM_PEAK_GBS, 4), "traffic": load_traffic("quantize"),
+                            "kernel": "quantize_pack_kernel<_Float16, 128>", "bytes_per_launch": quant_bytes(N, K)}}
+        if not a.no_cpu:
+            out["cpu_baseline"] = cpu_baseline_quantize()
+        line = json.dumps(out)
+        print(line, flush=True)
+        if a.json:
+            with open(a.json, "w") as f:
+                f.write(line + "\n")
         return 0
     pre = None
     dec = bench_decode(torch, gemm, a.steps, a.warmup) if a.workload == "decode" else None

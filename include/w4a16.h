@@ -97,6 +97,19 @@ int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
                  const uint16_t* scales, uint16_t* y, void* workspace, int32_t* counters,
                  void* stream);
 
+/* Quantise and pack a weight matrix on the device (asynchronous, no allocation).
+ * Replaces the reference's torch-side quantize_w4 + pack_int4 (tests/quant.py:62-74, 34-48),
+ * the producer of the Wp and scales that w4a16_gemm consumes:
+ *   W      : [N, K] row-major, fp16 (w_is_fp32 = 0) or fp32 (w_is_fp32 = 1), device memory.
+ *   Wp     : int32 [N*K/8] packed nibbles in the layout w4a16_launch reads.
+ *   scales : fp16 bits [K/G, N], s = fp16(max(absmax(group) / 7, 1e-4)).
+ * Codes q = clamp(round_half_even(W / s), -8, 7) + 8 with fp32 arithmetic, bit-identical to
+ * the reference's torch fp32 path.  N % 16 == 0, K % 64 == 0, G in {64, 128}; W and Wp
+ * 16-byte aligned.  Inputs must be finite (a NaN in a group gives unspecified codes).
+ * Returns W4A16_OK, W4A16_ERR_INVALID (message via w4a16_last_error) or W4A16_ERR_HIP. */
+int w4a16_quantize_pack(const void* W, int w_is_fp32, int64_t N, int64_t K, int64_t G,
+                        int32_t* Wp, uint16_t* scales, void* stream);
+
 /* Query the limits of HIP device `device` (cached per device, thread-safe). */
 int w4a16_query_device(int device, w4a16_device_limits* lim);
 

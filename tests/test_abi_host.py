@@ -226,3 +226,39 @@ def test_torch_binding_imports_and_rejects_host_tensors():
     with pytest.raises(RuntimeError, match="CUDA"):
         w4a16_opt.w4a16_gemm(torch.zeros(8, dtype=torch.int32), torch.zeros(1, 64, dtype=torch.half),
                              torch.zeros(1, 16, dtype=torch.half))
+
+
+@pytest.mark.parametrize("N,K,G,ptrs,msg", [
+    (24, 128, 64, (4096, 4096, 4096), "N must be a multiple of 16"),
+    (16, 96, 64, (4096, 4096, 4096), "K a multiple of 64"),
+    (16, 256, 32, (4096, 4096, 4096), "unsupported group size"),
+    (16, 256, 256, (4096, 4096, 4096), "unsupported group size"),
+    (-16, 256, 64, (4096, 4096, 4096), "dimensions out of range"),
+    (16, 1 << 31, 64, (4096, 4096, 4096), "dimensions out of range"),
+    (16, 128, 64, (0, 4096, 4096), "null pointer"),
+    (16, 128, 64, (4104, 4096, 4096), "16-byte aligned"),
+    (16, 128, 64, (4096, 4100, 4096), "16-byte aligned"),
+    (16, 128, 64, (4096, 4096, 4097), "2-byte aligned"),
+])
+def test_quantize_pack_validation(lib, N, K, G, ptrs, msg):
+    """w4a16_quantize_pack rejects bad arguments on the host, before touching the device."""
+    f = lib.w4a16_quantize_pack
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    rc = f(ptrs[0], 0, N, K, G, ptrs[1], ptrs[2], None)
+    assert rc == 1 and msg in lib.w4a16_last_error().decode()
+
+
+def test_quantize_pack_empty_is_a_no_op(lib):
+    f = lib.w4a16_quantize_pack
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    assert f(None, 0, 0, 128, 64, None, None, None) == 0
+    assert f(None, 1, 16, 0, 128, None, None, None) == 0
+
+
+def test_torch_quantize_pack_rejects_host_tensors():
+    torch = pytest.importorskip("torch")
+    import w4a16_opt
+    with pytest.raises(RuntimeError, match="CUDA"):
+        w4a16_opt.quantize_pack(torch.zeros(16, 128, dtype=torch.half), 64)

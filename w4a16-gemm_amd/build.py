@@ -45,7 +45,8 @@ def _run(cmd: list[str]) -> None:
 
 def build_lib() -> str:
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    srcs = [os.path.join(CSRC, "w4a16_kernels.hip"), os.path.join(CSRC, "w4a16_plan.cpp")]
+    srcs = [os.path.join(CSRC, "w4a16_kernels.hip"), os.path.join(CSRC, "w4a16_quantize.hip"),
+            os.path.join(CSRC, "w4a16_plan.cpp")]
     tmp = LIB + ".tmp"
     _run([hipcc, *HIPCC_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp])
     os.replace(tmp, LIB)

@@ -104,6 +104,27 @@ torch::Tensor w4a16_gemm(torch::Tensor Wp, torch::Tensor x, torch::Tensor scales
     return y;
 }
 
+// Device quantise + pack: the GPU replacement of the reference's quantize_w4 followed by
+// pack_int4 (tests/quant.py:62-74, 34-48).  Returns (Wp int32 [N*K/8], scales fp16 [K/G, N]).
+std::tuple<torch::Tensor, torch::Tensor> w4a16_quantize_pack_t(torch::Tensor W, int64_t group_size) {
+    TORCH_CHECK(W.is_cuda(), "W must be CUDA");
+    TORCH_CHECK(W.is_contiguous(), "contiguous only");
+    TORCH_CHECK(W.dtype() == torch::kHalf || W.dtype() == torch::kFloat, "W must be fp16 or fp32");
+    TORCH_CHECK(W.dim() == 2, "W must be [N, K]");
+    const int64_t N = W.size(0), K = W.size(1);
+    TORCH_CHECK(group_size > 0 && K % group_size == 0, "K must be a multiple of the group size");
+    const c10::DeviceGuard guard(W.device());
+    const int dev = W.device().index();
+    torch::Tensor Wp = torch::empty({N * K / 8}, W.options().dtype(torch::kInt32));
+    torch::Tensor scales = torch::empty({K / group_size, N}, W.options().dtype(torch::kHalf));
+    hipStream_t stream = c10::hip::getCurrentHIPStream(dev).stream();
+    const int rc = w4a16_quantize_pack(W.data_ptr(), W.dtype() == torch::kFloat ? 1 : 0, N, K, group_size,
+                                       Wp.data_ptr<int32_t>(), reinterpret_cast<uint16_t*>(scales.data_ptr()),
+                                       stream);
+    TORCH_CHECK(rc == W4A16_OK, "quantize_pack: ", w4a16_last_error());
+    return {Wp, scales};
+}
+
 // Introspection used by the tests and the benchmark: the plan the op would launch.
 py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t variant, int64_t device) {
     w4a16_problem prob;
@@ -147,5 +168,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("Wp"), py::arg("x"), py::arg("scales"), py::arg("variant") = -1);
     m.def("plan_info", &w4a16_plan_info, "Plan the op would launch for a shape (debug / bench)",
           py::arg("M"), py::arg("N"), py::arg("K"), py::arg("G"), py::arg("variant") = -1, py::arg("device") = 0);
+    m.def("quantize_pack", &w4a16_quantize_pack_t,
+          "Group-wise RTN int4 quantisation + packing on the device: W [N, K] -> (Wp, scales)",
+          py::arg("W"), py::arg("group_size"));
     m.attr("abi_version") = w4a16_abi_version();
 }
