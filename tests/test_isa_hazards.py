@@ -1,4 +1,4 @@
-"""CPU check of the gfx950 assembly of the decode kernels (compiled here with hipcc -S).
+"""CPU check of the gfx950 assembly of the library kernels (compiled here with hipcc -S).
 
 The decode LDS/stream/ring kernels and the wide prefill kernels issue loads through inline asm (global_load_* into VGPRs, ds_read_b128)
 so that the compiler's conservative waits do not serialise the weight stream.  The compiler does
@@ -11,7 +11,6 @@ from __future__ import annotations
 
 import os
 import re
-import shutil
 import subprocess
 
 import pytest
@@ -139,14 +138,23 @@ def check_kernel(lines):
 
 @pytest.fixture(scope="module")
 def isa(tmp_path_factory):
-    if not os.path.exists(HIPCC) or shutil.which("hipcc") is None and not os.path.exists(HIPCC):
+    """Device assembly of every HIP source of the library, compiled with its build flags."""
+    if not os.path.exists(HIPCC):
         pytest.skip("hipcc not available")
-    out = tmp_path_factory.mktemp("isa") / "k.s"
-    cmd = [HIPCC, "-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
-           "-packed-fp32-ops", f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}", "-S", "--cuda-device-only",
-           os.path.join(CSRC, "w4a16_kernels.hip"), "-o", str(out)]
-    subprocess.run(cmd, check=True, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
-    return out.read_text()
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "w4a16-gemm_amd"))
+    import build
+    d = tmp_path_factory.mktemp("isa")
+    text = []
+    for src, _ in build.SOURCES:
+        if not src.endswith(".hip"):
+            continue
+        out = d / (src + ".s")
+        flags = [f for f in build.compile_flags(src) if f != "-fPIC"]
+        subprocess.run([HIPCC, *flags, "-S", "--cuda-device-only", os.path.join(CSRC, src), "-o", str(out)],
+                       check=True, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+        text.append(out.read_text())
+    return "\n".join(text)
 
 
 def _kernels(text):
@@ -192,3 +200,38 @@ def test_no_bit_cast_of_vector_element():
 def test_no_kernel_spills(isa):
     sizes = re.findall(r"; ScratchSize: (\d+)", isa)
     assert sizes and all(int(s) == 0 for s in sizes), sizes
+
+
+def _loop_bodies(lines):
+    """Instruction texts of each innermost loop (from a 'Loop Header' label to its back-branch)."""
+    items, heads = [], []
+    for raw in lines:
+        t = raw.strip()
+        if "Loop Header" in t:
+            heads.append((len(items), t.split(":")[0]))
+        if not t or t.startswith(";") or (t.startswith(".") and "Loop Header" not in t):
+            continue
+        items.append(t)
+    loops = []
+    for start, label in heads:
+        end = next((i for i in range(start + 1, len(items)) if "cbranch" in items[i] and label in items[i]), None)
+        if end is not None:
+            loops.append(items[start:end + 1])
+    return loops
+
+
+def test_wide_prefill_accumulators_stay_in_place(isa):
+    """The wide prefill main loop keeps its MFMA accumulators in place: no accumulator register
+    copies or AGPR<->VGPR transfers (the default scheduler's allocation rotated them through
+    copies, serialising the MFMA pipe)."""
+    ks = {k: v for k, v in _kernels(isa).items() if "prefill_wide_kernel" in k}
+    assert len(ks) == 3, list(ks)
+    for name, lines in ks.items():
+        loops = [l for l in _loop_bodies(lines) if any("v_mfma" in t for t in l)]
+        assert len(loops) == 1, (name, len(loops))
+        ops = [t.split()[0] for t in loops[0]]
+        # two chunks of a 128 x 64 wave tile = 128 16x16x32 MFMAs' work (a 32x32x16 counts twice)
+        work = ops.count("v_mfma_f32_16x16x32_f16") + 2 * ops.count("v_mfma_f32_32x32x16_f16")
+        assert work == 128, (name, work)
+        moves = [o for o in ops if o.startswith("v_accvgpr")]
+        assert not moves, (name, len(moves))

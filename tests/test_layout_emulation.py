@@ -205,3 +205,131 @@ def test_decode_index_math(M, N, K, G, NBW, WAVES, splits):
                     y[li, n:n + 4] = fin[b, lane]
     assert not np.isnan(y).any()
     assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-12
+
+
+def mfma32(A, B, C):
+    """v_mfma_f32_32x32x16_f16 model.  A, B: [64 lanes, 8 slots] (lane (kg, r) holds row r of A /
+    column r of B at k = 8 kg + slot); C: [64 lanes, 16], register i of lane (kg, r) holds
+    C[8 (i // 4) + 4 kg + i % 4][r]."""
+    full = A[:32] @ B[:32].T + A[32:] @ B[32:].T
+    out = C.copy()
+    for lane in range(64):
+        kg, r = lane >> 5, lane & 31
+        for i in range(16):
+            out[lane, i] += full[8 * (i // 4) + 4 * kg + i % 4, r]
+    return out
+
+
+def wide_lane_block(nb0, q, r, nblk):
+    """prefill_wide_kernel: wave-uniform base block of channel block q and the lane's block offset
+    (both clamped to the last n16 block; the offset is 0 or 1)."""
+    qb = min(nb0 + 2 * q, nblk - 1)
+    return qb, min(nb0 + 2 * q + (r >> 4), nblk - 1) - qb
+
+
+@pytest.mark.parametrize("M,N,K,G,BM,BN,WMs,WNs", [
+    (40, 80, 256, 64, 128, 128, 1, 2), (70, 208, 384, 128, 128, 256, 1, 4), (33, 48, 128, 64, 256, 128, 2, 2),
+])
+def test_wide_prefill_32x32_index_math(M, N, K, G, BM, BN, WMs, WNs):
+    """prefill_wide_kernel on v_mfma_f32_32x32x16_f16: A lane (kg, r) of step (tp, h) is the
+    16x16x32 A lane (kb = 2 tp + kg, i = r % 16) of n16 block 2q + r / 16; B is read from the
+    permuted LDS row at h*64 + tp*32 + kg*16; D register i is channel 8(i/4) + 4kg + i%4."""
+    rng = np.random.default_rng(M * N)
+    q = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    s = rng.random((K // G, N)) * 0.05 + 0.001
+    x = rng.standard_normal((M, K))
+    W4 = quant.pack_int4(q).view(np.uint32).reshape(N // 16, K // 64, 32, 4)
+    ref = x @ ((q.astype(np.float64) - 8) * np.repeat(s.T, G, axis=1)).T
+    WM, WN = BM // WMs, BN // WNs
+    TM, TN = WM // 32, WN // 32
+    KC, NBLK = K // 64, N // 16
+    y = np.full((M, N), np.nan)
+    for tm in range(-(-M // BM)):
+        for tn in range(-(-N // BN)):
+            m0, n0 = tm * BM, tn * BN
+            accs = {}
+            for kc in range(KC):
+                lds = np.zeros(BM * XROW // 2)
+                for row in range(BM):
+                    for qseg in range(8):
+                        v = x[min(m0 + row, M - 1), kc * 64 + 8 * qseg: kc * 64 + 8 * qseg + 8]
+                        base = row * XROW + (qseg >> 2) * 64 + (qseg & 3) * 4
+                        for e in range(4):
+                            lds[(base + 16 * e) // 2:(base + 16 * e) // 2 + 2] = v[2 * e:2 * e + 2]
+                for wave in range(WMs * WNs):
+                    wm, wn = wave // WNs, wave % WNs
+                    nb0 = (n0 + wn * WN) >> 4
+                    for qq in range(TN):
+                        for h in range(2):
+                            for tp in range(2):
+                                A = np.zeros((64, 8))
+                                for lane in range(64):
+                                    kg, r = lane >> 5, lane & 31
+                                    qb, nbl = wide_lane_block(nb0, qq, r, NBLK)
+                                    nb = qb + nbl
+                                    Sn = s[kc * 64 // G, nb * 16:nb * 16 + 16]
+                                    A[lane] = a_operand(W4, Sn, nb, kc, h)[16 * (2 * tp + kg) + (r & 15)]
+                                for p in range(TM):
+                                    B = np.zeros((64, 8))
+                                    for lane in range(64):
+                                        kg, r = lane >> 5, lane & 31
+                                        off = ((wm * WM + p * 32 + r) * XROW + h * 64 + tp * 32 + kg * 16) // 2
+                                        B[lane] = lds[off:off + 8]
+                                    key = (wave, p, qq)
+                                    accs[key] = mfma32(A, B, accs.get(key, np.zeros((64, 16))))
+            for (wave, p, qq), C in accs.items():
+                wm, wn = wave // WNs, wave % WNs
+                nb0 = (n0 + wn * WN) >> 4
+                for lane in range(64):
+                    kg, r = lane >> 5, lane & 31
+                    m = m0 + wm * WM + p * 32 + r
+                    for g in range(4):
+                        if m < M and nb0 + 2 * qq + (g >> 1) < NBLK:
+                            n = (nb0 + 2 * qq) * 16 + 8 * g + 4 * kg
+                            y[m, n:n + 4] = C[lane, 4 * g:4 * g + 4]
+    assert not np.isnan(y).any()
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-12
+
+
+@pytest.mark.parametrize("cfg", [5, 6, 7])
+@pytest.mark.parametrize("M,N,K,G", [(300, 1040, 2048, 64), (129, 272, 1152, 64), (300, 80, 640, 64),
+                                     (513, 208, 384, 128), (70, 16, 128, 64), (40, 4112, 4160, 64)])
+def test_wide_prefill_addresses_in_bounds(cfg, M, N, K, G):
+    """Every global load and store offset of prefill_wide_kernel stays inside its buffer for shapes
+    whose last N tile is partial.  Regression: a per-lane block offset taken relative to an
+    unclamped base went negative and, as the unsigned 32-bit offset of a saddr load, addressed
+    4 GB past the weights."""
+    BM, BN, WMs, WNs = {5: (128, 256, 1, 4), 6: (256, 128, 2, 2), 7: (128, 128, 1, 2)}[cfg]
+    NT, WM, WN = WMs * WNs * 64, BM // WMs, BN // WNs
+    TM, TN = WM // 32, WN // 32
+    KC, NBLK, gshift = K // 64, N // 16, 1 if G == 128 else 0
+    sizes = {"w": N * K // 2, "s": (K // G) * N * 2, "x": M * K * 2, "y": M * N * 2}
+    for tile in range(-(-M // BM) * -(-N // BN)):
+        tm, tn = tile % -(-M // BM), tile // -(-M // BM)
+        m0, n0 = tm * BM, tn * BN
+        for wave in range(WMs * WNs):
+            wm, wn = wave // WNs, wave % WNs
+            nb0 = (n0 + wn * WN) >> 4
+            for lane in range(64):
+                kg, r = lane >> 5, lane & 31
+                for qq in range(TN):
+                    qb, nbl = wide_lane_block(nb0, qq, r, NBLK)
+                    assert nbl in (0, 1)
+                    for tp in range(2):
+                        woff = (nbl * KC * 512 + (((r & 7) << 2) | (tp << 1) | kg) * 16) & 0xFFFFFFFF
+                        for kcl in (0, KC - 1):
+                            assert qb * KC * 512 + kcl * 512 + woff + 16 <= sizes["w"]
+                    soff = ((nbl * 16 + (r & 15)) * 2) & 0xFFFFFFFF
+                    for kcl in (0, KC - 1):
+                        assert qb * 32 + (kcl >> gshift) * N * 2 + soff + 2 <= sizes["s"]
+                    for p in range(TM):
+                        m = m0 + wm * WM + p * 32 + r
+                        for g in range(4):
+                            n = (nb0 + 2 * qq) * 16 + 8 * g + 4 * kg
+                            if m < M and nb0 + 2 * qq + (g >> 1) < NBLK:
+                                assert n + 4 <= N and (m * N + n) * 2 + 8 <= sizes["y"]
+        for tid in range(NT):
+            for i in range(BM * 8 // NT):
+                sg = tid + i * NT
+                xoff = ((min(m0 + (sg >> 3), M - 1) - m0) * K + (sg & 7) * 8) * 2
+                assert m0 * K * 2 + (KC - 1) * 128 + xoff + 16 <= sizes["x"]

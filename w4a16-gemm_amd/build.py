@@ -43,12 +43,34 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
 
 
+# Sources of libw4a16_hip.so with their extra flags.  The wide prefill kernel is scheduled with
+# the max-memory-clause strategy: with the default strategy its 128 MFMA accumulators are rotated
+# through register copies inside the main loop (see the header of w4a16_prefill_wide.hip).
+SOURCES = [
+    ("w4a16_kernels.hip", []),
+    ("w4a16_prefill_wide.hip", ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]),
+    ("w4a16_quantize.hip", []),
+    ("w4a16_plan.cpp", []),
+]
+
+
+def compile_flags(src: str) -> list[str]:
+    """hipcc flags (without -c/-o) of one library source, also used by the assembly tests."""
+    extra = dict(SOURCES)[src]
+    return [*HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}"]
+
+
 def build_lib() -> str:
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    srcs = [os.path.join(CSRC, "w4a16_kernels.hip"), os.path.join(CSRC, "w4a16_quantize.hip"),
-            os.path.join(CSRC, "w4a16_plan.cpp")]
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    objs = []
+    for src, _ in SOURCES:
+        obj = os.path.join(objdir, src.rsplit(".", 1)[0] + ".o")
+        _run([hipcc, *compile_flags(src), "-c", os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
     tmp = LIB + ".tmp"
-    _run([hipcc, *HIPCC_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp])
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)
     return LIB
 

@@ -44,6 +44,17 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_32x32x16_f16: lane l supplies A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32]
+// (i = 0..7); D register i of lane l is D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].  Measured on
+// MI355X: one 16x16x32 MFMA over k-slots 0..31 equals two chained 16x16x16 MFMAs over slots
+// 0..15 then 16..31, and each of those equals the 32x32x16 MFMA over the same 16 slots, bit for
+// bit (the hardware rounds in the same k groups).  So kernels that feed the same k-slot sets in
+// the same order produce identical results whichever of the two shapes they use.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16 mfma32x32x16(h8 a, h8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 // Per-lane dequantisation constants (row i = lane % 16 selects the nibble parity).
 struct Dq {
     uint32_t mask;

@@ -11,6 +11,7 @@
 #include <cstring>
 
 #include "w4a16.h"
+#include "w4a16_asm.h"
 #include "w4a16_device.h"
 #include "w4a16_internal.h"
 
@@ -203,108 +204,6 @@ decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 // x fragments and scales first, then the DMAs pair by pair -- and (b) waits with an explicit
 // s_waitcnt vmcnt(#DMAs issued after pair p) before reading pair p.  Same tiling, reduction
 // and split-K hand-off as decode_kernel; KCW (chunks per wave) is a compile-time constant.
-// s_waitcnt vmcnt(n) for 0 <= n <= 63; n is a constant after unrolling, so this folds to one
-// instruction (larger n would wait for nothing: the kernels never issue more than 63 DMAs).
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    switch (n) {
-        case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-        case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
-        case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-        case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
-        case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-        case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
-        case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-        case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
-        case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-        case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
-        case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
-        case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
-        case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
-        case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
-        case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
-        case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
-        case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-        case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
-        case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
-        case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
-        case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
-        case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
-        case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
-        case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
-        case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-        case 25: asm volatile("s_waitcnt vmcnt(25)" ::: "memory"); break;
-        case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
-        case 27: asm volatile("s_waitcnt vmcnt(27)" ::: "memory"); break;
-        case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
-        case 29: asm volatile("s_waitcnt vmcnt(29)" ::: "memory"); break;
-        case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
-        case 31: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
-        case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
-        case 33: asm volatile("s_waitcnt vmcnt(33)" ::: "memory"); break;
-        case 34: asm volatile("s_waitcnt vmcnt(34)" ::: "memory"); break;
-        case 35: asm volatile("s_waitcnt vmcnt(35)" ::: "memory"); break;
-        case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
-        case 37: asm volatile("s_waitcnt vmcnt(37)" ::: "memory"); break;
-        case 38: asm volatile("s_waitcnt vmcnt(38)" ::: "memory"); break;
-        case 39: asm volatile("s_waitcnt vmcnt(39)" ::: "memory"); break;
-        case 40: asm volatile("s_waitcnt vmcnt(40)" ::: "memory"); break;
-        case 41: asm volatile("s_waitcnt vmcnt(41)" ::: "memory"); break;
-        case 42: asm volatile("s_waitcnt vmcnt(42)" ::: "memory"); break;
-        case 43: asm volatile("s_waitcnt vmcnt(43)" ::: "memory"); break;
-        case 44: asm volatile("s_waitcnt vmcnt(44)" ::: "memory"); break;
-        case 45: asm volatile("s_waitcnt vmcnt(45)" ::: "memory"); break;
-        case 46: asm volatile("s_waitcnt vmcnt(46)" ::: "memory"); break;
-        case 47: asm volatile("s_waitcnt vmcnt(47)" ::: "memory"); break;
-        case 48: asm volatile("s_waitcnt vmcnt(48)" ::: "memory"); break;
-        case 49: asm volatile("s_waitcnt vmcnt(49)" ::: "memory"); break;
-        case 50: asm volatile("s_waitcnt vmcnt(50)" ::: "memory"); break;
-        case 51: asm volatile("s_waitcnt vmcnt(51)" ::: "memory"); break;
-        case 52: asm volatile("s_waitcnt vmcnt(52)" ::: "memory"); break;
-        case 53: asm volatile("s_waitcnt vmcnt(53)" ::: "memory"); break;
-        case 54: asm volatile("s_waitcnt vmcnt(54)" ::: "memory"); break;
-        case 55: asm volatile("s_waitcnt vmcnt(55)" ::: "memory"); break;
-        case 56: asm volatile("s_waitcnt vmcnt(56)" ::: "memory"); break;
-        case 57: asm volatile("s_waitcnt vmcnt(57)" ::: "memory"); break;
-        case 58: asm volatile("s_waitcnt vmcnt(58)" ::: "memory"); break;
-        case 59: asm volatile("s_waitcnt vmcnt(59)" ::: "memory"); break;
-        case 60: asm volatile("s_waitcnt vmcnt(60)" ::: "memory"); break;
-        case 61: asm volatile("s_waitcnt vmcnt(61)" ::: "memory"); break;
-        case 62: asm volatile("s_waitcnt vmcnt(62)" ::: "memory"); break;
-        case 63: asm volatile("s_waitcnt vmcnt(63)" ::: "memory"); break;
-        default: break;
-    }
-}
-
-// Global loads the compiler does not track: the caller orders them with compiler barriers and
-// waits with explicit s_waitcnt vmcnt before reading the result registers.
-__device__ __forceinline__ u4 gload_u4_untracked(const void* p) {
-    u4 v;
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
-    return v;
-}
-__device__ __forceinline__ uint32_t gload_u16_untracked(const void* p) {
-    uint32_t v;
-    asm volatile("global_load_ushort %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
-    return v;
-}
-
-// After an explicit wait, re-define the registers of completed untracked loads through an empty
-// asm with in-out operands.  Without this the compiler treats an asm load's result as ready when
-// the asm issues: it may hoist uses above the wait or reuse the register while the load is still
-// in flight (an in-flight load later overwrote a reused address register: a wild address).
-// With it, each result stays live and untouched until the wait and is used only after it.
-template <typename T>
-__device__ __forceinline__ void bind_after_wait(T& v) {
-    asm volatile("" : "+v"(v));
-}
-
-// 16-byte LDS read the compiler does not track (the caller waits with s_waitcnt lgkmcnt(0)
-// and re-binds the result with bind_after_wait).
-__device__ __forceinline__ u4 lds_read_u4(uint32_t addr) {
-    u4 v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
-    return v;
-}
 
 template <int NBW, int WAVES, int KCW>
 __global__ void __launch_bounds__(WAVES * 64)
@@ -537,12 +436,6 @@ decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         for (int w = 1; w < WAVES; ++w) sum += reinterpret_cast<const f4*>(wl + w * WAVE_BYTES)[rb * 64 + lane];
     }
     decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
-}
-
-__device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
-    uint32_t v;
-    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr) : "memory");
-    return v;
 }
 
 // Decode with a refill-ahead ring of chunk pairs (kind 3).
@@ -865,211 +758,6 @@ prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     }
 }
 
-// Untracked loads with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte offset.
-__device__ __forceinline__ u4 gload_u4_sbase(const void* base, uint32_t off) {
-    u4 v;
-    asm volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(v) : "v"(off), "s"(base) : "memory");
-    return v;
-}
-__device__ __forceinline__ uint32_t gload_u16_sbase(const void* base, uint32_t off) {
-    uint32_t v;
-    asm volatile("global_load_ushort %0, %1, %2" : "=&v"(v) : "v"(off), "s"(base) : "memory");
-    return v;
-}
-
-// Prefill with large wave tiles (TM = WM/16 token blocks share each dequantised A operand).
-//
-// Same tile walk and MFMA order as prefill_kernel (every accumulator: chunk 0 h 0, chunk 0 h 1,
-// chunk 1 h 0, ...; identical A and B operands), so its output is bit-identical to every other
-// prefill config.  Differences that cut the vector-ALU work per MFMA:
-//  * each A operand (one n16 block, one chunk half) feeds TM = WM/16 MFMAs, so dequantisation
-//    costs 14/TM VALU per MFMA;
-//  * the weights of chunk kc+2 are loaded while chunk kc is multiplied, into two named register
-//    sets used alternately (the loop is unrolled by two chunks, K/64 must be even), so no
-//    register copies;
-//  * rows past M and blocks past N load clamped, in-bounds data instead of branching (their
-//    results are never stored and rows never mix);
-//  * XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so block b is
-//    given tile (b % 8) * (G / 8) + b / 8: each XCD walks consecutive tiles, i.e. the M tiles
-//    that share a weight tile, through its own L2.
-template <int BM, int BN, int WAVES_M, int WAVES_N>
-__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
-prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
-                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                    int M, int N, int K, int gshift, int tiles_m) {
-    constexpr int NT = WAVES_M * WAVES_N * 64;
-    constexpr int WM = BM / WAVES_M;
-    constexpr int WN = BN / WAVES_N;
-    constexpr int TM = WM / 16;
-    constexpr int TN = WN / 16;
-    constexpr int XBUF = BM * kXRow;
-    constexpr int SEGS = BM * 8;
-    constexpr int SPT = SEGS / NT;
-    static_assert(WM % 16 == 0 && WN % 16 == 0 && SEGS % NT == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) char xs[2 * XBUF];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);      // wave-uniform (SGPR)
-    const int wm = wave / WAVES_N;
-    const int wn = wave - wm * WAVES_N;
-    const int kb = lane >> 4;
-    const int li = lane & 15;
-
-    // XCD-aware tile order (a bijection on [0, gridDim.x)).
-    const int G = gridDim.x;
-    const int G8 = G >> 3;
-    const int b = blockIdx.x;
-    const int tile = b < (G8 << 3) ? (b & 7) * G8 + (b >> 3) : b;
-    const int tm = tile % tiles_m;
-    const int tn = tile / tiles_m;
-    const int m0 = tm * BM;
-    const int n0 = tn * BN;
-    const int KC = K >> 6;
-    const int NBLK = N >> 4;
-    const int nb0 = (n0 >> 4) + wn * TN;
-    const int lanep = ((li & 7) << 2) | kb;
-
-    // All global loads are issued through asm with a wave-uniform base (SGPRs, advanced per
-    // chunk) and a constant 32-bit per-lane byte offset, and waited for with explicit counts: the
-    // compiler's own wait placement drained every prefetch at the loop back-edge.
-    const char* wbase[TN];
-    const char* sbase[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int nbc = min(nb0 + j, NBLK - 1);
-        wbase[j] = reinterpret_cast<const char*>(Wp + (size_t)nbc * KC * 32);
-        sbase[j] = reinterpret_cast<const char*>(scales + (size_t)nbc * 16);
-    }
-    const uint32_t woff = (uint32_t)lanep * 16;
-    const uint32_t soff = (uint32_t)li * 2;
-    const char* xbase = reinterpret_cast<const char*>(x + (size_t)m0 * K);
-    uint32_t xoff[SPT];                                        // bytes, relative to row m0, chunk 0
-#pragma unroll
-    for (int r = 0; r < SPT; ++r) {
-        const int sg = tid + r * NT;
-        xoff[r] = ((uint32_t)(min(m0 + (sg >> 3), M - 1) - m0) * (uint32_t)K + (sg & 7) * 8) * 2;
-    }
-
-    u4 xr0[SPT], xr1[SPT];
-    auto load_x = [&](int kc, u4 (&xr)[SPT]) {
-        const char* xb = xbase + (size_t)min(kc, KC - 1) * 128;   // past the end: harmless reload
-#pragma unroll
-        for (int r = 0; r < SPT; ++r) xr[r] = gload_u4_sbase(xb, xoff[r]);
-    };
-    auto store_x = [&](int buf, u4 (&xr)[SPT]) {
-#pragma unroll
-        for (int r = 0; r < SPT; ++r) bind_after_wait(xr[r]);
-#pragma unroll
-        for (int r = 0; r < SPT; ++r) {
-            const int sg = tid + r * NT;
-            lds_store_xseg(xs + buf * XBUF + (sg >> 3) * kXRow, sg & 7, xr[r]);
-        }
-    };
-    u4 w0[TN], w1[TN];
-    uint32_t s0[TN], s1[TN];
-    auto load_w = [&](int kc, u4 (&w)[TN], uint32_t (&s)[TN]) {
-        const int kcl = min(kc, KC - 1);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) w[j] = gload_u4_sbase(wbase[j] + (size_t)kcl * 512, woff);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) s[j] = gload_u16_sbase(sbase[j] + (size_t)(kcl >> gshift) * N * 2, soff);
-    };
-    // Loads younger than x of chunk c+1 when chunk c starts (weights c, x c+2, weights c+1), and
-    // younger than the weights of chunk c once x of chunk c+3 is issued (x c+2, weights c+1,
-    // x c+3): see the issue order below.
-    constexpr int WAIT_X = 4 * TN + SPT;
-    constexpr int WAIT_W = 2 * SPT + 2 * TN;
-    static_assert(WAIT_X <= 63 && WAIT_W <= 63, "vmcnt range");
-
-    f4 acc[TM][TN];
-#pragma unroll
-    for (int t = 0; t < TM; ++t)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[t][j] = f4{0.f, 0.f, 0.f, 0.f};
-
-    const Dq d = dq_setup(lane);
-    const uint32_t xrow = (uint32_t)reinterpret_cast<uintptr_t>(xs) + (wm * WM + li) * kXRow + kb * 16;
-    // One chunk: for each half h, all TM B operands are read from LDS through asm (the compiler
-    // would interleave each read with a full lgkmcnt wait), the TN A operands are dequantised
-    // while the reads are in flight, then one wait and the TM x TN MFMAs.
-    auto compute = [&](int buf, u4 (&w)[TN], uint32_t (&s)[TN]) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) { bind_after_wait(w[j]); bind_after_wait(s[j]); }
-        const uint32_t xb = xrow + buf * XBUF;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            u4 bv[TM];
-#pragma unroll
-            for (int t = 0; t < TM; ++t) bv[t] = lds_read_u4(xb + t * 16 * kXRow + h * 64);
-            h8 a[TN];
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const h2 s2 = scale2((uint16_t)s[j]);
-                a[j] = h ? dq_frag(w[j].z, w[j].w, d, s2) : dq_frag(w[j].x, w[j].y, d, s2);
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-            for (int t = 0; t < TM; ++t) bind_after_wait(bv[t]);
-#pragma unroll
-            for (int t = 0; t < TM; ++t) {
-                const h8 bf = __builtin_bit_cast(h8, bv[t]);
-#pragma unroll
-                for (int j = 0; j < TN; ++j) acc[t][j] = mfma16x16x32(a[j], bf, acc[t][j]);
-            }
-        }
-    };
-
-    // Issue order: prologue x0 | x1 w0 x2 w1; then chunk c issues x(c+3) and w(c+2).  Chunk c
-    // uses x buffer c & 1, x register set and weight set c & 1 (the loop is unrolled by two
-    // chunks; K/64 is even, checked by the planner).  x of chunk c+1 is written to the other LDS
-    // buffer first, so those LDS writes overlap the MFMAs.  One barrier per chunk orders both
-    // buffers.  Loads past the end re-read the last chunk into registers nobody uses again.
-    load_x(0, xr0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    store_x(0, xr0);
-    load_x(1, xr1);
-    load_w(0, w0, s0);
-    load_x(2, xr0);
-    load_w(1, w1, s1);
-    __syncthreads();
-    for (int kc = 0; kc < KC; kc += 2) {
-        wait_vmcnt(WAIT_X);
-        store_x(1, xr1);
-        load_x(kc + 3, xr1);
-        wait_vmcnt(WAIT_W);
-        compute(0, w0, s0);
-        load_w(kc + 2, w0, s0);
-        __syncthreads();
-        wait_vmcnt(WAIT_X);
-        store_x(0, xr0);
-        load_x(kc + 4, xr0);
-        wait_vmcnt(WAIT_W);
-        compute(1, w1, s1);
-        load_w(kc + 3, w1, s1);
-        __syncthreads();
-    }
-    // No load in flight at exit.  The registers of the last (unused) prefetches are re-bound
-    // after the wait: otherwise the compiler, seeing them dead, reuses them before it.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int r = 0; r < SPT; ++r) { bind_after_wait(xr0[r]); bind_after_wait(xr1[r]); }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        bind_after_wait(w0[j]); bind_after_wait(s0[j]); bind_after_wait(w1[j]); bind_after_wait(s1[j]);
-    }
-
-#pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        const int m = m0 + wm * WM + t * 16 + li;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int n = (nb0 + j) * 16 + 4 * kb;
-            if (m < M && nb0 + j < NBLK) *reinterpret_cast<u2*>(y + (size_t)m * N + n) = pack_f16x4(acc[t][j]);
-        }
-    }
-}
-
 // Small-M prefill (17 <= M <= 16*TM): one wave per n16 block walks the whole K range.
 //
 // With few token rows the prefill tiles leave most CUs idle (N/BN workgroups) and a K-sequential
@@ -1210,6 +898,11 @@ prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 
 // ------------------------------------------------------------------------------------ launch
 
+// Wide prefill configs (kind 1) live in their own translation unit (w4a16_prefill_wide.hip),
+// compiled with a different instruction-scheduling strategy.
+hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
+                               uint16_t* y, hipStream_t st);
+
 template <int CFG> struct PrefillCfg;
 #define W4A16_PREFILL_CFG(ID)                                                                  \
     template <> struct PrefillCfg<ID> {                                                        \
@@ -1237,8 +930,7 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
         hipLaunchKernelGGL((prefill_stream_kernel<C::BM / 16, kPrefillTable[CFG].depth>), dim3(p.grid), dim3(64), 0, st,
                            Wp, x, s, y, p.M, p.N, p.K, gshift);
     else if constexpr (kPrefillTable[CFG].kind == 1)
-        hipLaunchKernelGGL((prefill_wide_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
-                           dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
+        return launch_prefill_wide(CFG, p, Wp, x, s, y, st);
     else
         hipLaunchKernelGGL((prefill_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
                            dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);

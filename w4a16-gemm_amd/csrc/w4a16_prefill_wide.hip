@@ -1,0 +1,275 @@
+// Wide-tile prefill (configs 5..7 of kPrefillTable, kind 1) in its own translation unit.
+//
+// Built with -mllvm -amdgpu-sched-strategy=max-memory-clause (build.py): with the default
+// scheduler the register allocator gives most MFMAs a destination other than their accumulator
+// input and rotates the 128 accumulators through copies (96 v_accvgpr_mov plus 56 AGPR<->VGPR
+// transfers per two chunks, which serialise the MFMA pipe); with this strategy every
+// accumulator stays in place in 128 AGPRs and the loop body is ~30% shorter.  The decode and
+// other prefill kernels keep the default scheduler (the strategy does not help them).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "w4a16.h"
+#include "w4a16_asm.h"
+#include "w4a16_device.h"
+#include "w4a16_internal.h"
+
+namespace w4a16 {
+
+// Prefill with large wave tiles on v_mfma_f32_32x32x16_f16.
+//
+// Wave tile WM x WN (tokens x channels) = TM x TN blocks of 32 x 32.  Per 64-wide K chunk and
+// chunk half h the k-slots of the 16x16x32 formulation (k = 32h + 8c + 2t + e, t = 0..3) are fed
+// as two 32x32x16 steps, t in {0, 1} then t in {2, 3}: lane (kg = l / 32, r = l % 32) supplies
+// t = 2 tp + kg.  Measured on MI355X, this gives every accumulator bit for bit the same value as
+// the 16x16x32 kernels (see mfma32x32x16), so all prefill configs stay bit-identical.  One
+// 32x32x16 instruction does the work of two 16x16x32 ones, which halves the MFMA issue slots per
+// chunk: with one wave per SIMD the wave's instruction stream (MFMA issue + dequantisation VALU +
+// memory) and not the matrix pipe limited the 16x16x32 version.
+//  * A (weights, rows = channels): lane (kg, r) reads the 16-byte word quad of packed lane
+//    4 (r % 8) + 2 tp + kg of n16 block 2q + r / 16 and keeps the nibbles of its own channel
+//    (odd pairs for r % 16 >= 8), exactly as the 16x16x32 kernels do; the word quad gives the A
+//    operands of both halves of the chunk.
+//  * B (x, columns = tokens): one 16-byte LDS read per (token block, tp, h) from the permuted x
+//    layout shared with the other prefill kernels (dword 16h + 4t + c).
+//  * D: register i of lane (kg, r) holds channel 8 (i / 4) + 4 kg + i % 4 of token r: four runs
+//    of four consecutive channels, each one 8-byte fp16 store.
+//  * The weights of chunk kc+2 are loaded while chunk kc is multiplied, into two named register
+//    sets used alternately (the loop is unrolled by two chunks, K/64 must be even).
+//  * Rows past M and channels past N load clamped, in-bounds data instead of branching (their
+//    results are never stored and rows never mix).
+//  * XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so block b is
+//    given tile (b % 8) * (G / 8) + b / 8: each XCD walks consecutive tiles, i.e. the M tiles
+//    that share a weight tile, through its own L2.
+template <int BM, int BN, int WAVES_M, int WAVES_N>
+__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
+prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
+                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
+                    int M, int N, int K, int gshift, int tiles_m) {
+    constexpr int NT = WAVES_M * WAVES_N * 64;
+    constexpr int WM = BM / WAVES_M;
+    constexpr int WN = BN / WAVES_N;
+    constexpr int TM = WM / 32;
+    constexpr int TN = WN / 32;
+    constexpr int XBUF = BM * kXRow;
+    constexpr int SEGS = BM * 8;
+    constexpr int SPT = SEGS / NT;
+    static_assert(WM % 32 == 0 && WN % 32 == 0 && SEGS % NT == 0, "tile shape");
+    __shared__ __attribute__((aligned(16))) char xs[2 * XBUF];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);      // wave-uniform (SGPR)
+    const int wm = wave / WAVES_N;
+    const int wn = wave - wm * WAVES_N;
+    const int kg = lane >> 5;
+    const int r = lane & 31;
+
+    // XCD-aware tile order (a bijection on [0, gridDim.x)).
+    const int G = gridDim.x;
+    const int G8 = G >> 3;
+    const int b = blockIdx.x;
+    const int tile = b < (G8 << 3) ? (b & 7) * G8 + (b >> 3) : b;
+    const int tm = tile % tiles_m;
+    const int tn = tile / tiles_m;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    const int KC = K >> 6;
+    const int NBLK = N >> 4;
+    const int nb0 = (n0 + wn * WN) >> 4;                            // first n16 block of the wave
+
+    // All global loads are issued through asm with a wave-uniform base (SGPRs, advanced per
+    // chunk) and a constant 32-bit per-lane byte offset, and waited for with explicit counts: the
+    // compiler's own wait placement drained every prefetch at the loop back-edge.
+    // The wave-uniform base is the first n16 block of the 32-channel block q and the lane adds 0
+    // or 1 block (r / 16), both clamped to the last block of N, so the unsigned 32-bit lane offset
+    // is never negative (blocks past N re-read the last block; their results are never stored).
+    const char* wbase[TN];
+    const char* sbase[TN];
+    int qblk[TN];
+#pragma unroll
+    for (int q = 0; q < TN; ++q) {
+        qblk[q] = min(nb0 + 2 * q, NBLK - 1);
+        wbase[q] = reinterpret_cast<const char*>(Wp + (size_t)qblk[q] * KC * 32);
+        sbase[q] = reinterpret_cast<const char*>(scales + (size_t)qblk[q] * 16);
+    }
+    uint32_t woff[TN][2];
+    uint32_t soff[TN];
+#pragma unroll
+    for (int q = 0; q < TN; ++q) {
+        const int nbl = min(nb0 + 2 * q + (r >> 4), NBLK - 1) - qblk[q];          // 0 or 1
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+            woff[q][tp] = (uint32_t)(nbl * KC * 512 + (((r & 7) << 2) | (tp << 1) | kg) * 16);
+        soff[q] = (uint32_t)((nbl * 16 + (r & 15)) * 2);
+    }
+    const char* xbase = reinterpret_cast<const char*>(x + (size_t)m0 * K);
+    uint32_t xoff[SPT];                                        // bytes, relative to row m0, chunk 0
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+        const int sg = tid + i * NT;
+        xoff[i] = ((uint32_t)(min(m0 + (sg >> 3), M - 1) - m0) * (uint32_t)K + (sg & 7) * 8) * 2;
+    }
+
+    u4 xr0[SPT], xr1[SPT];
+    auto load_x = [&](int kc, u4 (&xr)[SPT]) {
+        const char* xb = xbase + (size_t)min(kc, KC - 1) * 128;   // past the end: harmless reload
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) xr[i] = gload_u4_sbase(xb, xoff[i]);
+    };
+    auto store_x = [&](int buf, u4 (&xr)[SPT]) {
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) bind_after_wait(xr[i]);
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int sg = tid + i * NT;
+            lds_store_xseg(xs + buf * XBUF + (sg >> 3) * kXRow, sg & 7, xr[i]);
+        }
+    };
+    u4 w0[TN][2], w1[TN][2];
+    uint32_t s0[TN], s1[TN];
+    auto load_w = [&](int kc, u4 (&w)[TN][2], uint32_t (&s)[TN]) {
+        const int kcl = min(kc, KC - 1);
+#pragma unroll
+        for (int q = 0; q < TN; ++q)
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp) w[q][tp] = gload_u4_sbase(wbase[q] + (size_t)kcl * 512, woff[q][tp]);
+#pragma unroll
+        for (int q = 0; q < TN; ++q) s[q] = gload_u16_sbase(sbase[q] + (size_t)(kcl >> gshift) * N * 2, soff[q]);
+    };
+    // Per chunk: SPT x loads and 3 TN weight/scale loads.  Loads younger than x of chunk c+1 when
+    // chunk c starts: weights c, x c+2, weights c+1; younger than the weights of chunk c once x of
+    // chunk c+3 is issued: x c+2, weights c+1, x c+3.
+    constexpr int WAIT_X = 6 * TN + SPT;
+    constexpr int WAIT_W = 2 * SPT + 3 * TN;
+    static_assert(WAIT_X <= 63 && WAIT_W <= 63, "vmcnt range");
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int p = 0; p < TM; ++p)
+#pragma unroll
+        for (int q = 0; q < TN; ++q)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[p][q][i] = 0.f;
+
+    const Dq d = dq_setup(r);                                  // nibble parity of channel r % 16
+    const uint32_t xrow = (uint32_t)reinterpret_cast<uintptr_t>(xs) + (wm * WM + r) * kXRow + kg * 16;
+    // One chunk: for each half h, the 2 TM B operands are read from LDS through asm (the compiler
+    // would follow each read with a full lgkmcnt wait), the 2 TN A operands are dequantised
+    // while the reads are in flight, then one wait and the 4 TM TN MFMAs (tp = 0 before tp = 1).
+    auto compute = [&](int buf, u4 (&w)[TN][2], uint32_t (&s)[TN]) {
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+            bind_after_wait(w[q][0]); bind_after_wait(w[q][1]); bind_after_wait(s[q]);
+        }
+        const uint32_t xb = xrow + buf * XBUF;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            u4 bv[TM][2];
+#pragma unroll
+            for (int p = 0; p < TM; ++p)
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp) bv[p][tp] = lds_read_u4(xb + p * 32 * kXRow + h * 64 + tp * 32);
+            h8 a[TN][2];
+#pragma unroll
+            for (int q = 0; q < TN; ++q) {
+                const h2 s2 = scale2((uint16_t)s[q]);
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp)
+                    a[q][tp] = h ? dq_frag(w[q][tp].z, w[q][tp].w, d, s2) : dq_frag(w[q][tp].x, w[q][tp].y, d, s2);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int p = 0; p < TM; ++p) { bind_after_wait(bv[p][0]); bind_after_wait(bv[p][1]); }
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int p = 0; p < TM; ++p) {
+                    const h8 bf = __builtin_bit_cast(h8, bv[p][tp]);
+#pragma unroll
+                    for (int q = 0; q < TN; ++q) acc[p][q] = mfma32x32x16(a[q][tp], bf, acc[p][q]);
+                }
+        }
+    };
+
+    // Issue order: prologue x0 | x1 w0 x2 w1; then chunk c issues x(c+3) and w(c+2).  Chunk c
+    // uses x buffer c & 1, x register set and weight set c & 1 (the loop is unrolled by two
+    // chunks; K/64 is even, checked by the planner).  x of chunk c+1 is written to the other LDS
+    // buffer first, so those LDS writes overlap the MFMAs.  One barrier per chunk orders both
+    // buffers.  Loads past the end re-read the last chunk into registers nobody uses again.
+    load_x(0, xr0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    store_x(0, xr0);
+    load_x(1, xr1);
+    load_w(0, w0, s0);
+    load_x(2, xr0);
+    load_w(1, w1, s1);
+    __syncthreads();
+    for (int kc = 0; kc < KC; kc += 2) {
+        wait_vmcnt(WAIT_X);
+        store_x(1, xr1);
+        load_x(kc + 3, xr1);
+        wait_vmcnt(WAIT_W);
+        compute(0, w0, s0);
+        load_w(kc + 2, w0, s0);
+        __syncthreads();
+        wait_vmcnt(WAIT_X);
+        store_x(0, xr0);
+        load_x(kc + 4, xr0);
+        wait_vmcnt(WAIT_W);
+        compute(1, w1, s1);
+        load_w(kc + 3, w1, s1);
+        __syncthreads();
+    }
+    // No load in flight at exit.  The registers of the last (unused) prefetches are re-bound
+    // after the wait: otherwise the compiler, seeing them dead, reuses them before it.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) { bind_after_wait(xr0[i]); bind_after_wait(xr1[i]); }
+#pragma unroll
+    for (int q = 0; q < TN; ++q) {
+        bind_after_wait(w0[q][0]); bind_after_wait(w0[q][1]); bind_after_wait(s0[q]);
+        bind_after_wait(w1[q][0]); bind_after_wait(w1[q][1]); bind_after_wait(s1[q]);
+    }
+
+#pragma unroll
+    for (int p = 0; p < TM; ++p) {
+        const int m = m0 + wm * WM + p * 32 + r;
+        if (m >= M) continue;
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int nbk = nb0 + 2 * q + (g >> 1);
+                const int n = (nb0 + 2 * q) * 16 + 8 * g + 4 * kg;
+                if (nbk < NBLK)
+                    *reinterpret_cast<u2*>(y + (size_t)m * N + n) =
+                        pack_f16x4(f4{acc[p][q][4 * g], acc[p][q][4 * g + 1], acc[p][q][4 * g + 2], acc[p][q][4 * g + 3]});
+            }
+        }
+    }
+}
+
+template <int CFG>
+static hipError_t launch_wide(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s, uint16_t* y,
+                              hipStream_t st) {
+    constexpr PrefillTile c = kPrefillTable[CFG];
+    static_assert(c.kind == 1, "wide prefill configs only");
+    const int gshift = p.G == 128 ? 1 : 0;
+    const int tiles_m = (p.M + c.bm - 1) / c.bm;
+    hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n>), dim3(p.grid),
+                       dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
+                               uint16_t* y, hipStream_t st) {
+    switch (cfg) {
+        case 5: return launch_wide<5>(p, Wp, x, s, y, st);
+        case 6: return launch_wide<6>(p, Wp, x, s, y, st);
+        case 7: return launch_wide<7>(p, Wp, x, s, y, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace w4a16
