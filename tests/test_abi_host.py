@@ -173,6 +173,7 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (128, 14336, 4096, None),                                                # too few wide tiles
     (17, 4096, 14336, 8), (32, 14336, 4096, 8), (33, 4096, 4096, 9), (64, 4096, 4096, 9),  # few token rows
     (48, 14336, 4096, None),                                                 # many blocks: 16 x 128 tiles
+    (32, 28672, 4096, None),                                                 # N/16 > 4 CUs: tiles
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)

@@ -81,10 +81,11 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         return tiles >= 2.0 * cus * occ && tiles <= (double)std::numeric_limits<int32_t>::max() ? tiles : -1.0;
     };
     // Few token rows: one wave per n16 block over the whole K (prefill_stream_kernel) instead of
-    // tiles that leave most CUs idle.  Measured on MI355X: faster for every N at M <= 32 (e.g.
-    // K = 14336, N = 4096: 53 vs 154 us), and at M <= 64 when N/16 blocks are at most twice the
-    // CU count (at N = 14336, M = 48 the 16 x 128 tiles win).
-    if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K)) return 8;
+    // tiles that leave most CUs idle.  Measured on MI355X: faster at M <= 32 while N/16 blocks
+    // are at most 4x the CU count (K = 14336, N = 4096: 53 vs 154 us; N = 14336: 34 vs 45 us; at
+    // N = 28672 the 32 x 128 tiles win, 49 vs 65 us), and at M <= 64 while they are at most twice
+    // the CU count (at N = 14336, M = 48 the 16 x 128 tiles win).
+    if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K) && N / 16 <= 4 * lim.cu_count) return 8;
     if (prefill_occupancy(9, lim) > 0 && prefill_shape_ok(9, M, K) && N / 16 <= 2 * lim.cu_count) return 9;
     int occ5 = 0;
     const double t5 = wide_tiles(5, occ5);
