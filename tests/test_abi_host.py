@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 9
+        assert 1 <= p.kernel <= 11
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -163,17 +163,18 @@ def test_prefill_plan_invariants(lib, M, N):
 
 
 PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128),
-                 8: (32, 16), 9: (64, 16)}
+                 8: (32, 16), 9: (64, 16), 10: (32, 64), 11: (64, 64)}
 
 
 @pytest.mark.parametrize("M,N,K,want", [
     (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
     (2048, 14336, 4096, 7),                                                  # partial last round: 128x128
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
-    (128, 14336, 4096, None),                                                # too few wide tiles
-    (17, 4096, 14336, 8), (32, 14336, 4096, 8), (33, 4096, 4096, 9), (64, 4096, 4096, 9),  # few token rows
-    (48, 14336, 4096, None),                                                 # many blocks: 16 x 128 tiles
-    (32, 28672, 4096, None),                                                 # N/16 > 4 CUs: tiles
+    (17, 4096, 14336, 8), (32, 14336, 4096, 8),                              # few token rows, few blocks
+    (33, 4096, 4096, 10), (64, 4096, 4096, 10), (128, 4096, 14336, 10),      # token groups of 32
+    (32, 28672, 4096, 10), (48, 14336, 4096, 10),
+    (128, 14336, 4096, 11), (512, 4096, 4096, 11),                           # token groups of 64
+    (512, 6144, 4096, 7), (128, 28672, 4096, 7),                             # moderate sizes: 128x128 wide
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
@@ -184,7 +185,7 @@ def test_prefill_wide_selection(lib, M, N, K, want):
         assert p.kernel == want
     tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
-    assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1}[p.kernel]
+    assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4}[p.kernel]
 
 
 def test_prefill_override(lib, monkeypatch):

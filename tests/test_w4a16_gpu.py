@@ -435,14 +435,15 @@ def test_prefill_wide_configs_bitwise_equal(cfg, M, N, K, G, monkeypatch):
     assert torch.equal(gemm(Wp, x[:M // 2 + 1].contiguous(), scales), y[:M // 2 + 1])
 
 
-# Small-M prefill (M = 17..64, chosen automatically): one wave per n16 block over the whole K,
-# bit-identical to the reference-API variants.
+# Small-M prefill (M = 17..64, chosen automatically): one wave per n16 block over the whole K
+# (alone, or sharing the x rows of a token group), bit-identical to the reference-API variants.
 @pytest.mark.parametrize("M,N,K,G", [(17, 4096, 4096, 128), (32, 1040, 2048, 64), (33, 256, 1024, 128),
                                      (64, 272, 1024, 64), (20, 16, 1024, 64), (40, 512, 14336, 128)])
 def test_prefill_small_m_bitwise_equal(M, N, K, G):
     torch = torch_cuda()
     import w4a16_opt
-    assert "prefill_stream_kernel" in w4a16_opt.plan_info(M, N, K, G)["kernel_name"]
+    name = w4a16_opt.plan_info(M, N, K, G)["kernel_name"]
+    assert "prefill_stream_kernel" in name or "prefill_group_kernel" in name, name
     x, q, scales, Wp, key = make_problem(M, N, K, G, seed=M)
     y = gemm(Wp, x, scales)
     assert torch.equal(y, gemm(Wp, x, scales, variant=4))
@@ -451,3 +452,27 @@ def test_prefill_small_m_bitwise_equal(M, N, K, G):
     for m in (17, M - 1):
         if 17 <= m < M:
             assert torch.equal(gemm(Wp, x[:m].contiguous(), scales), y[:m]), m
+
+
+# Token-group prefill (configs 10, 11, forced through W4A16_PREFILL): 4 waves share the x rows of
+# a group of 32 or 64 tokens; any M, N tails (waves past N compute clamped data and store nothing).
+@pytest.mark.parametrize("cfg", [10, 11])
+@pytest.mark.parametrize("M,N,K,G", [(17, 4096, 4096, 128), (33, 1040, 2048, 64), (100, 272, 1024, 64),
+                                     (300, 4112, 4224, 64), (1000, 512, 2048, 128), (64, 16, 1024, 128),
+                                     (129, 6144, 4096, 128)])
+def test_prefill_token_groups_bitwise_equal(monkeypatch, cfg, M, N, K, G):
+    torch = torch_cuda()
+    import w4a16_opt
+    print(f"token-group prefill cfg={cfg} M={M} N={N} K={K} G={G}", flush=True)
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=M + cfg)
+    ref4 = gemm(Wp, x, scales, variant=4)
+    monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+    info = w4a16_opt.plan_info(M, N, K, G)
+    assert info["kernel"] == cfg and "prefill_group_kernel" in info["kernel_name"], info
+    y = gemm(Wp, x, scales)
+    assert torch.equal(y, ref4)
+    assert torch.equal(y, gemm(Wp, x, scales, variant=1))
+    assert_close(y, ref_gemm(x, q, scales, G, key))
+    m = max(17, M // 3)                                       # M <= 16 would route to decode
+    if m < M:
+        assert torch.equal(gemm(Wp, x[:m].contiguous(), scales), y[:m])

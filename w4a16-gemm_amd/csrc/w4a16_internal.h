@@ -9,12 +9,14 @@ namespace w4a16 {
 // PfCfg<1..4>, src/vectorized/kernel.cu:59-63, re-tiled for 64-wide wavefronts and 256 CUs) and
 // run prefill_kernel (kind 0); ids 5..7 run prefill_wide_kernel (kind 1, wave tile 128 x 64);
 // ids 8..9 run prefill_stream_kernel (kind 2: one wave per n16 block over the whole K, for
-// M <= bm, ring of `depth` chunk pairs).  The auto planner (or the W4A16_PREFILL override)
-// picks among all of them; all give bit-identical output.
+// M <= bm, ring of `depth` chunk pairs); ids 10..11 run prefill_group_kernel (kind 3: waves_n
+// waves, one per n16 block, share the x rows of a group of bm tokens in the ring; any M, one
+// token group per grid row).  The auto planner (or the W4A16_PREFILL override) picks among all
+// of them; all give bit-identical output.
 struct PrefillTile {
     int bm, bn, waves_m, waves_n, kind, depth;
 };
-constexpr PrefillTile kPrefillTable[10] = {
+constexpr PrefillTile kPrefillTable[12] = {
     {0, 0, 0, 0, 0, 0},
     {16, 128, 1, 4, 0, 0},     // 1: small batches: 4 waves across N, wave tile 16 x 32
     {32, 128, 1, 4, 0, 0},     // 2: wave tile 32 x 32
@@ -25,24 +27,30 @@ constexpr PrefillTile kPrefillTable[10] = {
     {128, 128, 1, 2, 1, 0},    // 7: wave tile 128 x 64, 2 waves
     {32, 16, 1, 1, 2, 6},      // 8: M <= 32, one wave per n16 block, 6 pairs in flight
     {64, 16, 1, 1, 2, 3},      // 9: M <= 64, one wave per n16 block, 3 pairs in flight
+    {32, 64, 1, 4, 3, 3},      // 10: groups of 32 tokens, 4 n16 blocks per workgroup, 3 pairs
+    {64, 64, 1, 4, 3, 2},      // 11: groups of 64 tokens, 4 n16 blocks per workgroup, 2 pairs
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 9;      // all prefill configs
+constexpr int kNumPrefillTable = 11;     // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;
 
+// Ring slot of kinds 2 and 3: per wave 1 KB of weights and 1 KB of scales, plus the x rows of the
+// token group (bm rows x 256 B).
 constexpr int prefill_lds_bytes(int cfg) {
-    return kPrefillTable[cfg].kind == 2
-               ? (kPrefillTable[cfg].depth + 1) * (2048 + kPrefillTable[cfg].bm / 4 * 1024)   // ring slots
+    return kPrefillTable[cfg].kind >= 2
+               ? (kPrefillTable[cfg].depth + 1) *
+                     (2048 * kPrefillTable[cfg].waves_n + kPrefillTable[cfg].bm / 4 * 1024)   // ring slots
                : 2 * kPrefillTable[cfg].bm * kLdsRowBytes;
 }
-// Kinds 1 and 2 walk K two chunks at a time; kind 2 covers all M in one tile and needs at least
-// `depth` chunk pairs.
+// Kinds 1..3 walk K two chunks at a time; kinds 2 and 3 need at least `depth` chunk pairs and
+// kind 2 covers all M in one tile.
 constexpr bool prefill_shape_ok(int cfg, int M, int K) {
     return kPrefillTable[cfg].kind == 0 ||
            ((K / 64) % 2 == 0 &&
-            (kPrefillTable[cfg].kind != 2 || (M <= kPrefillTable[cfg].bm && K / 128 >= kPrefillTable[cfg].depth)));
+            (kPrefillTable[cfg].kind < 2 ||
+             ((kPrefillTable[cfg].kind == 3 || M <= kPrefillTable[cfg].bm) && K / 128 >= kPrefillTable[cfg].depth)));
 }
 constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n; }
 

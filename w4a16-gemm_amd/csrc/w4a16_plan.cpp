@@ -80,13 +80,25 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         return tiles >= 2.0 * cus * occ && tiles <= (double)std::numeric_limits<int32_t>::max() ? tiles : -1.0;
     };
-    // Few token rows: one wave per n16 block over the whole K (prefill_stream_kernel) instead of
-    // tiles that leave most CUs idle.  Measured on MI355X: faster at M <= 32 while N/16 blocks
-    // are at most 4x the CU count (K = 14336, N = 4096: 53 vs 154 us; N = 14336: 34 vs 45 us; at
-    // N = 28672 the 32 x 128 tiles win, 49 vs 65 us), and at M <= 64 while they are at most twice
-    // the CU count (at N = 14336, M = 48 the 16 x 128 tiles win).
+    // Rules measured on MI355X (graph-timed sweep of every config over M = 17..1024 on the
+    // Llama-3-8B projection shapes):
+    //  * M <= 32 while N/16 blocks are at most 4x the CU count: one wave per n16 block over the
+    //    whole K (prefill_stream_kernel; K = 14336, N = 4096: 52 vs 155 us for 16 x 128 tiles);
+    //  * token groups of 32 rows, 4 waves sharing x (prefill_group_kernel), while the waves
+    //    (M/32 groups x N/16 blocks) are at most 12 per CU: e.g. K = 14336, N = 4096, M = 128:
+    //    65 vs 152 us; N = 28672, M = 32: 31 vs 49 us;
+    //  * token groups of 64 rows while those waves are at most 8 per CU (N = 4096, M = 512: 43 vs
+    //    46 us; N = 28672, M = 64: 45 vs 50 us);
+    //  * then the wide tiles, which beat the 16..128-row tiles for every larger size measured
+    //    (N = 6144, M = 512: 54 vs 73 us).
+    const double blocks = std::ceil(N / 16.0);
     if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K) && N / 16 <= 4 * lim.cu_count) return 8;
-    if (prefill_occupancy(9, lim) > 0 && prefill_shape_ok(9, M, K) && N / 16 <= 2 * lim.cu_count) return 9;
+    if (prefill_occupancy(10, lim) > 0 && prefill_shape_ok(10, M, K) &&
+        std::ceil(M / 32.0) * blocks <= 12.0 * cus)
+        return 10;
+    if (prefill_occupancy(11, lim) > 0 && prefill_shape_ok(11, M, K) &&
+        std::ceil(M / 64.0) * blocks <= 8.0 * cus)
+        return 11;
     int occ5 = 0;
     const double t5 = wide_tiles(5, occ5);
     if (t5 > 0 && std::fmod(t5, cus * occ5) == 0.0) return 5;
@@ -94,9 +106,10 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         int occ = 0;
         if (wide_tiles(cfg, occ) > 0) return cfg;
     }
+    if (prefill_occupancy(7, lim) > 0 && prefill_shape_ok(7, M, K)) return 7;
     for (int cfg = kNumPrefillTable; cfg >= 1; --cfg) {    // descending: ties go to the later config
         const int occ = prefill_occupancy(cfg, lim);
-        if (occ < 1 || !prefill_shape_ok(cfg, M, K) || kPrefillTable[cfg].kind == 2) continue;   // kind 2: rule above
+        if (occ < 1 || !prefill_shape_ok(cfg, M, K) || kPrefillTable[cfg].kind >= 1) continue;   // other kinds: rules above
         const PrefillTile& t = kPrefillTable[cfg];
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         if (tiles > (double)std::numeric_limits<int32_t>::max()) continue;
