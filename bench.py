@@ -13,6 +13,8 @@ timed region.  The calls are captured in HIP graphs (as the reference benchmark 
 graphs, benchmarks/bench_gemm.py:36-56) and timed with HIP events on the launch stream.
 
 Second leg: prefill TFLOP/s at M=2048, K=8192, N=28672, G=128.
+Third leg: prefill at moderate batch, M=128, K=4096, N=14336, G=64,
+reported against both rooflines (its arithmetic intensity sits just above the ridge point).
 
 Algorithmic work (the roofline numerator): bytes = N*K/2 + (K/G)*N*2 + M*K*2 + M*N*2 per call,
 flops = 2*M*N*K per call.  Peaks: HBM 8000 GB/s, fp16 dense MFMA 2500 TFLOP/s (MI355X spec).
@@ -42,6 +44,7 @@ MALL_BYTES = 256 * 2**20
 DECODE_CASES = [("gate_up", 14336, 4096, m) for m in (1, 4, 8, 16)] + \
                [("down", 4096, 14336, m) for m in (1, 4, 8, 16)]
 PREFILL_CASE = ("mlp70b", 28672, 8192, 2048)
+MODERATE_CASE = ("gate_up", 14336, 4096, 128, 64)          # M=128, G=64
 G = 128
 
 
@@ -57,7 +60,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_weights(torch, N, K, seed, copies):
+def make_weights(torch, N, K, seed, copies, G=G):
     """BASELINE distributions: q ~ U{0..15} packed in the reference layout, scales ~ U[0.002, 0.02].
     The packing runs once on the host (oracle.quant.pack_int4 is only data preparation here); the
     copies are device clones."""
@@ -149,6 +152,24 @@ def bench_prefill(torch, gemm, steps, warmup):
     log(f"prefill {name} M={M}: {us:.1f} us  {tfs:.1f} TFLOP/s")
     import w4a16_opt
     return {"us": us, "TFLOPs": tfs, "steps": steps, "kernel": w4a16_opt.plan_info(M, N, K, G)["kernel_name"]}
+
+
+def bench_moderate(torch, gemm, steps, warmup):
+    """BASELINE configs[2] (prefill at moderate batch: M=128, K=4096, N=14336, G=64): arithmetic
+    intensity ~419 flop/B, just above the MI355X ridge (~315 flop/B), so both rooflines apply."""
+    name, N, K, M, Gm = MODERATE_CASE
+    copies = max(2, -(-2 * MALL_BYTES // (N * K // 2 + (K // Gm) * N * 2)))
+    w = make_weights(torch, N, K, 104, copies, G=Gm)
+    x = torch.randn(M, K, device="cuda").half()
+    graphs = [graph_of(torch, [lambda Wp=Wp, s=s: gemm(Wp, x, s) for Wp, s in w])]
+    ms = time_graph(torch, graphs, steps, warmup)
+    us = ms * 1e3 / (steps * len(w))
+    tfs = alg_flops(M, N, K) / (us * 1e-6) / 1e12
+    gbs = alg_bytes(M, N, K, Gm) / (us * 1e-6) / 1e9
+    log(f"moderate {name} M={M} G={Gm}: {us:.1f} us  {tfs:.1f} TFLOP/s  {gbs:.0f} GB/s")
+    import w4a16_opt
+    return {"us": us, "TFLOPs": tfs, "GBs": gbs, "copies": len(w),
+            "kernel": w4a16_opt.plan_info(M, N, K, Gm)["kernel_name"]}
 
 
 def bench_copy(torch, steps):
@@ -318,6 +339,7 @@ def main(argv=None) -> int:
     if a.workload == "prefill" or not a.no_prefill:
         pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
                             a.warmup if a.workload == "prefill" else 3)
+    mod = bench_moderate(torch, gemm, 30, 3) if (dec is not None and not a.no_prefill) else None
 
     out = {"metric": "decode GB/s & %HBM peak (M=1..16); prefill TFLOP/s & %MFMA peak (M=2048)"}
     if dec is not None:
@@ -343,7 +365,11 @@ def main(argv=None) -> int:
                    "roofline": {"bound": "mfma", "achieved": round(pre["TFLOPs"], 1), "peak": FP16_MFMA_PEAK_TFS,
                                 "unit": "TFLOP/s", "frac": round(pre["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
                                 "traffic": load_traffic("prefill"), "kernel": pre["kernel"],
-                                "flops_per_launch": alg_flops(M, N, K)}}
+                                "flops_per_launch": alg_flops(M, N, K),
+                                # rocprofv3 counters of the same kernel (profiles/):
+                                # SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)
+                                "mfma_busy_frac": load_traffic("prefill_mfma_util"),
+                                "clock_ghz": load_traffic("prefill_clock_ghz")}}
         if dec is None:
             out.update({"value": pre_obj["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps,
                         "warmup": a.warmup, "ms_per_step": round(pre["us"] / 1e3, 5), "higher_is_better": True,
@@ -351,6 +377,17 @@ def main(argv=None) -> int:
                         "data": "synthetic", "config": pre_obj["config"], "roofline": pre_obj["roofline"]})
         else:
             out["prefill"] = pre_obj
+    if mod is not None:
+        _, N, K, M, Gm = MODERATE_CASE
+        out["moderate"] = {
+            "value": round(mod["TFLOPs"], 1), "unit": "TFLOP/s", "us_per_call": round(mod["us"], 2),
+            "GB_per_s": round(mod["GBs"], 1),
+            "config": {"workload": "BASELINE configs[2]: prefill M=128 K=4096 N=14336 G=64",
+                       "weight_copies": mod["copies"]},
+            "roofline": {"bound": "both (intensity ~419 flop/B, ridge ~315)", "kernel": mod["kernel"],
+                         "frac_mfma": round(mod["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
+                         "frac_hbm": round(mod["GBs"] / HBM_PEAK_GBS, 4),
+                         "flops_per_launch": alg_flops(M, N, K), "bytes_per_launch": alg_bytes(M, N, K, Gm)}}
     if not a.no_cpu:
         if dec is not None:
             out["cpu_baseline"] = cpu_baseline(DECODE_CASES)

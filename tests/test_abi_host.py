@@ -264,3 +264,20 @@ def test_torch_quantize_pack_rejects_host_tensors():
     import w4a16_opt
     with pytest.raises(RuntimeError, match="CUDA"):
         w4a16_opt.quantize_pack(torch.zeros(16, 128, dtype=torch.half), 64)
+
+
+def test_bandwidth_probe_loads_and_rejects_bad_arguments():
+    """The streaming-read probe behind measure_bw.py: exported, and it refuses arguments it
+    cannot launch on (null pointers, no workgroups, a size that is not whole 16-byte words)
+    before touching the device."""
+    path = os.path.join(ROOT, "w4a16-gemm_amd", "libw4a16_bwprobe.so")
+    if not os.path.exists(path):
+        pytest.fail(f"{path} not built (python w4a16-gemm_amd/build.py)")
+    f = ctypes.CDLL(path).w4a16_bw_read
+    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    assert f(None, 1024, 16, 8, None) == 1
+    assert f(16, 1024, None, 8, None) == 1
+    assert f(16, 1024, 16, 0, None) == 1
+    assert f(16, 1000, 16, 8, None) == 1
+    assert f(8, 1024, 16, 8, None) == 1

@@ -75,6 +75,18 @@ def build_lib() -> str:
     return LIB
 
 
+PROBE = os.path.join(HERE, "libw4a16_bwprobe.so")
+
+
+def build_probe() -> str:
+    """The streaming-read probe of measure_bw.py (a separate tool library, not the GEMM ABI)."""
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    tmp = PROBE + ".tmp"
+    _run([hipcc, *HIPCC_FLAGS, "-shared", os.path.join(CSRC, "bw_probe.hip"), "-o", tmp])
+    os.replace(tmp, PROBE)
+    return PROBE
+
+
 def build_ext() -> str:
     import torch.utils.cpp_extension as ce
     import torch
@@ -104,6 +116,7 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     build_lib()
     if not a.lib:
+        build_probe()
         build_ext()
     return 0
 
