@@ -267,17 +267,24 @@ def test_torch_quantize_pack_rejects_host_tensors():
 
 
 def test_bandwidth_probe_loads_and_rejects_bad_arguments():
-    """The streaming-read probe behind measure_bw.py: exported, and it refuses arguments it
-    cannot launch on (null pointers, no workgroups, a size that is not whole 16-byte words)
-    before touching the device."""
+    """The read and copy probes behind measure_bw.py: exported, and they refuse arguments they
+    cannot launch on (null pointers, an empty or non-16-byte-multiple size, a misaligned
+    buffer) before touching the device."""
     path = os.path.join(ROOT, "w4a16-gemm_amd", "libw4a16_bwprobe.so")
     if not os.path.exists(path):
         pytest.fail(f"{path} not built (python w4a16-gemm_amd/build.py)")
-    f = ctypes.CDLL(path).w4a16_bw_read
-    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
-    f.restype = ctypes.c_int
-    assert f(None, 1024, 16, 8, None) == 1
-    assert f(16, 1024, None, 8, None) == 1
-    assert f(16, 1024, 16, 0, None) == 1
-    assert f(16, 1000, 16, 8, None) == 1
-    assert f(8, 1024, 16, 8, None) == 1
+    L = ctypes.CDLL(path)
+    rd, cp = L.w4a16_bw_read, L.w4a16_bw_copy
+    rd.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    cp.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    rd.restype = cp.restype = ctypes.c_int
+    assert rd(None, 1024, 16, None) == 1
+    assert rd(16, 1024, None, None) == 1
+    assert rd(16, 0, 16, None) == 1
+    assert rd(16, 1000, 16, None) == 1
+    assert rd(8, 1024, 16, None) == 1
+    assert cp(None, 16, 1024, None) == 1
+    assert cp(16, None, 1024, None) == 1
+    assert cp(16, 32, 0, None) == 1
+    assert cp(16, 32, 1000, None) == 1
+    assert cp(16, 40, 1024, None) == 1

@@ -333,3 +333,114 @@ def test_wide_prefill_addresses_in_bounds(cfg, M, N, K, G):
                 sg = tid + i * NT
                 xoff = ((min(m0 + (sg >> 3), M - 1) - m0) * K + (sg & 7) * 8) * 2
                 assert m0 * K * 2 + (KC - 1) * 128 + xoff + 16 <= sizes["x"]
+
+
+def ring_x_rows(x, M, K, kc0, p, XR):
+    """decode_ring_kernel x rows of pair p as they land in LDS: XR rows x 64 dwords (each dword a
+    pair of fp64 halves).  XR == 1: one 4-byte load, lane j fetching dword 32*(u/8) + 16*((u/4)%2)
+    + 4*(j%4) + u%4 of the pair (u = j / 4).  XR >= 4: 16-byte loads of 4 rows each, lane j of
+    load q filling row (64q + j) / 16, segment j % 16 with global segment (j % 16) ^ (row % 8).
+    Also returns the largest source byte offset touched within an x row."""
+    slot = np.empty((XR, 64, 2))
+    hi = 0
+    if XR == 1:
+        for lane in range(64):
+            u = lane >> 2
+            d = 32 * (u >> 3) + 16 * ((u >> 2) & 1) + 4 * (lane & 3) + (u & 3)
+            off = kc0 * 128 + p * 256 + 4 * d
+            hi = max(hi, off + 4)
+            slot[0, lane] = x[0, off // 2:off // 2 + 2]
+        return slot, hi
+    for q in range(XR // 4):
+        for lane in range(64):
+            r = (64 * q + lane) >> 4
+            gseg = (lane & 15) ^ (r & 7)
+            off = kc0 * 128 + p * 256 + gseg * 16
+            hi = max(hi, off + 16)
+            for e in range(4):
+                slot[r, 4 * (lane & 15) + e] = x[min(r, M - 1), off // 2 + 2 * e:off // 2 + 2 * e + 2]
+    return slot, hi
+
+
+def ring_b_operand(slot, M, XR, cc, h):
+    """B operand (64 lanes x 8 halves) and the LDS byte address of each lane's first dword."""
+    B = np.zeros((64, 8))
+    addr = []
+    for lane in range(64):
+        kb, j = lane >> 4, lane & 15
+        xr = min(j, M - 1)
+        if XR == 1:
+            pos = 8 * cc + 4 * h + kb
+            B[lane] = slot[0, 4 * pos:4 * pos + 4].reshape(8)
+            addr.append(pos * 16)
+        else:
+            dws = []
+            for c in range(4):
+                pos = 8 * cc + ((4 * h + c) ^ (xr & 7))
+                dws.append(slot[xr, 4 * pos + kb])
+                if c == 0:
+                    addr.append(xr * 256 + pos * 16 + 4 * kb)
+            B[lane] = np.concatenate(dws)
+    return B, addr
+
+
+@pytest.mark.parametrize("M,N,K,G,NBW,WAVES,splits", [
+    (1, 64, 1024, 64, 1, 8, 1), (1, 128, 2048, 128, 2, 4, 2), (2, 64, 1024, 128, 1, 4, 2),
+    (3, 128, 1024, 128, 2, 4, 2), (5, 64, 1024, 64, 1, 4, 1), (9, 64, 2048, 128, 4, 4, 1),
+    (16, 64, 1024, 64, 2, 4, 2),
+])
+def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
+    """decode_ring_kernel x paths (4-byte loads in B-operand order for M = 1, swizzled 16-byte
+    loads plus four 4-byte LDS reads otherwise) with the weights as in decode_kernel: the emulated
+    result equals the float64 matmul, every x source offset stays inside the row, every B operand
+    holds x[row][32h + 8c + 2kb + {0,1}] in slot pair c, and the first-dword reads of 8 consecutive
+    lanes with 8 distinct rows hit 8 distinct 16-byte bank groups."""
+    rng = np.random.default_rng(M * 11 + K)
+    q = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    s = rng.random((K // G, N)) * 0.05 + 0.001
+    x = rng.standard_normal((M, K))
+    W4 = quant.pack_int4(q).view(np.uint32).reshape(N // 16, K // 64, 32, 4)
+    ref = x @ ((q.astype(np.float64) - 8) * np.repeat(s.T, G, axis=1)).T
+    XR = 1 if M <= 1 else 4 if M <= 4 else 8 if M <= 8 else 16
+    KC = K // 64
+    kcw = KC // (splits * WAVES)
+    y = np.full((M, N), np.nan)
+    for tile in range(N // (16 * NBW)):
+        fin = np.zeros((NBW, 64, 4))
+        for split in range(splits):
+            for wave in range(WAVES):
+                kc0 = (split * WAVES + wave) * kcw
+                acc = np.zeros((NBW, 64, 4))
+                for p in range(kcw // 2):
+                    slot, hi = ring_x_rows(x, M, K, kc0, p, XR)
+                    assert hi <= 2 * K
+                    for cc in range(2):
+                        Bs = []
+                        for h in range(2):
+                            B, addr = ring_b_operand(slot, M, XR, cc, h)
+                            for lane in range(64):
+                                kb, j = lane >> 4, lane & 15
+                                base = (kc0 + 2 * p + cc) * 64 + 32 * h + 2 * kb
+                                want = [x[min(j, M - 1), base + 8 * c + e] for c in range(4) for e in range(2)]
+                                assert np.array_equal(B[lane], want)
+                            for g0 in range(0, 64, 8):
+                                rows = {min(j, M - 1) for j in range(g0 & 15, (g0 & 15) + 8)}
+                                if len(rows) == 8:
+                                    assert len({a // 16 % 8 for a in addr[g0:g0 + 8]}) == 8
+                            Bs.append(B)
+                        kc = kc0 + 2 * p + cc
+                        for b in range(NBW):
+                            nb = tile * NBW + b
+                            Sn = s[kc * 64 // G, nb * 16:nb * 16 + 16]
+                            for h in range(2):
+                                acc[b] = mfma(a_operand(W4, Sn, nb, kc, h), Bs[h], acc[b])
+                fin += acc
+        for b in range(NBW):
+            nb = tile * NBW + b
+            for lane in range(64):
+                li = lane & 15
+                if li < M:
+                    n = nb * 16 + 4 * (lane >> 4)
+                    y[li, n:n + 4] = fin[b, lane]
+    assert not np.isnan(y).any()
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-12

@@ -371,8 +371,20 @@ DECODE_FORCED += [(v, sp, N, K) for v, sp, N, K in [
 DECODE_FORCED_G = [(v, sp, N, K, 128) for v, sp, N, K in DECODE_FORCED] + [
     (24, 1, 256, 4096, 64), (27, 2, 256, 4096, 64), (26, 1, 512, 2048, 64), (30, 2, 256, 4096, 64),
     (28, 2, 256, 14336, 64)]
-# shape 31 has no ring that fits LDS for 9..16 token rows: forced only for M <= 8
-DECODE_FORCED_SMALL_M = [(31, 1, 256, 4096, 128), (31, 2, 256, 4096, 64)]
+DECODE_FORCED_G += [(v, sp, N, K, 128) for v, sp, N, K in [
+    (34, 1, 256, 4096), (36, 1, 256, 4096), (36, 7, 256, 14336)]] + [
+    (34, 2, 256, 14336, 64), (36, 2, 256, 4096, 64)]
+# Ring shapes whose LDS ring holds fewer than 16 token rows: forced only up to their row limit
+# (the planner refuses them above it).  (variant, splits, N, K, G, largest M)
+DECODE_FORCED_SMALL_M = [
+    (31, 1, 256, 4096, 128, 8), (31, 2, 256, 4096, 64, 8),
+    (32, 1, 256, 4096, 128, 8), (32, 1, 256, 14336, 128, 8), (32, 1, 256, 4096, 64, 8),
+    (33, 1, 256, 4096, 128, 8), (33, 2, 256, 14336, 128, 8), (33, 1, 256, 4096, 64, 8),
+    (35, 1, 256, 14336, 128, 1), (35, 1, 512, 14336, 64, 1),
+    (37, 1, 256, 4096, 128, 8), (37, 2, 256, 14336, 128, 8),
+    (38, 1, 256, 14336, 128, 4), (38, 1, 512, 14336, 64, 4),
+    (39, 1, 256, 4096, 128, 8), (39, 2, 256, 14336, 64, 8),
+]
 
 
 @pytest.mark.parametrize("v,splits,N,K,G", DECODE_FORCED_G)
@@ -384,25 +396,25 @@ def test_decode_shapes_forced(v, splits, N, K, G, monkeypatch):
     assert info["decode_variant"] == v and info["splits"] == splits, info
     x, q, scales, Wp, key = make_problem(16, N, K, G, seed=v + 31)
     Wd = dequant_f32(key)
-    for M in (1, 3, 5, 9, 16):
+    for M in (1, 2, 3, 5, 9, 16):
         xm = x[:M].contiguous()
         assert_close(gemm(Wp, xm, scales, variant=0), ref_gemm(xm, q, scales, G, key))
     _onehot_decode_check(Wp, scales, Wd, K, v, splits, 16)
 
 
-@pytest.mark.parametrize("v,splits,N,K,G", DECODE_FORCED_SMALL_M)
-def test_decode_shapes_forced_small_m(v, splits, N, K, G, monkeypatch):
+@pytest.mark.parametrize("v,splits,N,K,G,mmax", DECODE_FORCED_SMALL_M)
+def test_decode_shapes_forced_small_m(v, splits, N, K, G, mmax, monkeypatch):
     torch = torch_cuda()
     import w4a16_opt
     monkeypatch.setenv("W4A16_DECODE", f"{v},{splits}")
-    info = w4a16_opt.plan_info(8, N, K, G, 0)
+    info = w4a16_opt.plan_info(mmax, N, K, G, 0)
     assert info["decode_variant"] == v and info["splits"] == splits, info
-    assert w4a16_opt.plan_info(16, N, K, G, 0)["decode_variant"] != v    # does not fit: not planned
-    x, q, scales, Wp, key = make_problem(8, N, K, G, seed=v + 37)
-    for M in (1, 4, 8):
+    assert w4a16_opt.plan_info(mmax + 1, N, K, G, 0)["decode_variant"] != v    # does not fit: not planned
+    x, q, scales, Wp, key = make_problem(mmax, N, K, G, seed=v + 37)
+    for M in sorted({1, min(2, mmax), (mmax + 1) // 2, mmax}):
         xm = x[:M].contiguous()
         assert_close(gemm(Wp, xm, scales, variant=0), ref_gemm(xm, q, scales, G, key))
-    _onehot_decode_check(Wp, scales, dequant_f32(key), K, v, splits, 8)
+    _onehot_decode_check(Wp, scales, dequant_f32(key), K, v, splits, mmax)
 
 
 def _onehot_decode_check(Wp, scales, Wd, K, v, splits, m):

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "w4a16_device.h"
 
 namespace w4a16 {
@@ -119,6 +121,49 @@ __device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
     uint32_t v;
     asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr) : "memory");
     return v;
+}
+
+// The same untracked LDS reads at addr + OFF, with OFF in the instruction's 16-bit offset field
+// (no address arithmetic per read).
+template <int OFF>
+__device__ __forceinline__ u4 lds_read_u4_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
+    u4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_u32_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_u16_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+
+// Compile-time loops: f(std::integral_constant<int, i>{}) for i = B .. E-1, so that indices can
+// feed template arguments (immediate offsets above).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// f(std::integral_constant<int, r>{}) for a runtime r in [I, E).
+template <int I, int E, typename F>
+__device__ __forceinline__ void static_switch(int r, F&& f) {
+    if constexpr (I < E) {
+        if (r == I) f(std::integral_constant<int, I>{});
+        else static_switch<I + 1, E>(r, f);
+    }
 }
 
 // Untracked loads with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte offset.

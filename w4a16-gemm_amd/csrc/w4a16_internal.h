@@ -62,13 +62,13 @@ constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m 
 //                                  (exactly d chunks per wave);
 //   kind 2: decode_stream_kernel  per-wave ring of d chunk pairs in LDS (the pairs per wave must
 //                                  be a multiple of d);
-//   kind 3: decode_ring_kernel    ring of d + 1 chunk-pair slots (weights and x rows), d pairs in
-//                                  flight also while computing; scales of the wave's K range in
-//                                  LDS (pairs per wave >= d, groups per wave * nbw <= 64).
+//   kind 3: decode_ring_kernel    ring of d + 1 chunk-pair slots (weights, x rows and the pair's
+//                                  scales), d pairs in flight also while computing (pairs per
+//                                  wave >= d).
 struct DecodeCfg {
     int kind, nbw, waves, d;
 };
-constexpr DecodeCfg kDecodeTable[32] = {
+constexpr DecodeCfg kDecodeTable[40] = {
     {0, 1, 16, 4}, {0, 1, 16, 2}, {0, 2, 16, 4}, {0, 2, 16, 2},     // 0-3
     {0, 1, 8, 4},  {0, 2, 8, 4},  {0, 4, 8, 4},  {0, 4, 16, 2},     // 4-7
     {1, 4, 16, 4}, {1, 4, 8, 8},  {1, 4, 8, 7},  {1, 2, 16, 7},     // 8-11
@@ -77,18 +77,21 @@ constexpr DecodeCfg kDecodeTable[32] = {
     {2, 4, 4, 2},  {2, 2, 8, 4},  {2, 1, 8, 4},  {2, 4, 8, 2},      // 20-23
     {3, 4, 4, 2},  {3, 4, 4, 3},  {3, 4, 8, 1},  {3, 1, 8, 2},      // 24-27
     {3, 2, 4, 2},  {3, 1, 4, 4},  {3, 2, 8, 1},  {3, 4, 4, 4},      // 28-31
+    {3, 1, 16, 2}, {3, 1, 8, 4},  {3, 2, 8, 2},  {3, 1, 16, 4},     // 32-35
+    {3, 2, 4, 4},  {3, 1, 8, 3},  {3, 2, 16, 2}, {3, 4, 8, 2},      // 36-39
 };
-constexpr int kNumDecodeCfg = 32;
+constexpr int kNumDecodeCfg = 40;
 
-// x-row loads per chunk pair of the kind-3 kernel: 4 token rows each.
-constexpr int decode_ring_xd(int M) { return M <= 4 ? 1 : M <= 8 ? 2 : 4; }
+// Token rows per chunk-pair slot of the kind-3 kernel: one row for M = 1 (4-byte x loads in
+// B-operand order), else 4, 8 or 16 rows (16-byte x loads of 4 rows each).
+constexpr int decode_ring_xr(int M) { return M <= 1 ? 1 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
 constexpr int decode_lds_bytes(int v, int M) {
     return kDecodeTable[v].kind == 0   ? kDecodeTable[v].waves * kDecodeTable[v].nbw * 64 * 16 + 16
            : kDecodeTable[v].kind == 1 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * ((kDecodeTable[v].d + 1) / 2) * 1024 + 16
            : kDecodeTable[v].kind == 2 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * kDecodeTable[v].d * 1024 + 16
-                                       : kDecodeTable[v].waves *
-                                             (2048 + (kDecodeTable[v].d + 1) * (kDecodeTable[v].nbw + decode_ring_xd(M)) * 1024) + 16;
+                                       : kDecodeTable[v].waves * (kDecodeTable[v].d + 1) *
+                                             (kDecodeTable[v].nbw * 1088 + decode_ring_xr(M) * 256) + 16;
 }
 // Whether a decode shape can cover K (in 64-wide chunks, group size G) with `splits` workgroups
 // per column tile.
@@ -98,8 +101,7 @@ constexpr bool decode_shape_fits(int v, int KC, int splits, int G) {
            (kDecodeTable[v].kind != 2 || ((KC / (splits * kDecodeTable[v].waves)) % (2 * kDecodeTable[v].d) == 0)) &&
            (kDecodeTable[v].kind != 3 ||
             ((KC / (splits * kDecodeTable[v].waves)) % 2 == 0 &&
-             KC / (splits * kDecodeTable[v].waves) >= 2 * kDecodeTable[v].d &&
-             (KC / (splits * kDecodeTable[v].waves)) / (G / 64) * kDecodeTable[v].nbw <= 64));
+             KC / (splits * kDecodeTable[v].waves) >= 2 * kDecodeTable[v].d));
 }
 
 // Counter buffer size (ints) the library may ask for: one per decode column tile.

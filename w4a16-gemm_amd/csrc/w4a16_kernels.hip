@@ -445,18 +445,31 @@ decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 //  * The ring has D + 1 slots and the loads of pair p + D are issued BEFORE pair p is
 //    dequantised and multiplied, so the memory system always holds D pairs of every wave,
 //    also while the wave computes.
-//  * A pair's x rows (4*XD rows; rows >= M repeat row M-1) arrive in the slot by direct-to-LDS
-//    loads next to the weights, 16-byte segments XOR-swizzled by row so that the B-operand reads
-//    of 16 token rows hit distinct bank groups.  The scales of the wave's whole K range
-//    ([group][block][16 channels]) arrive by two direct-to-LDS loads before the ring starts
-//    (groups * NBW <= 64, checked by the planner).  Per pair the wave issues NBW + XD memory
-//    instructions (4 + 3*NBW in decode_stream_kernel).
+//  * A pair's x rows (XR rows; rows >= M repeat row M-1) arrive in the slot by direct-to-LDS
+//    loads next to the weights.  The B operand of lane (kb, j) for MFMA half h of chunk cc is
+//    dwords 16h + 4c + kb (c = 0..3) of row j's chunk, a stride-4 gather:
+//      - XR >= 4 (M >= 2): 16-byte loads of 4 rows each (XR/4 per pair), 16-byte segments
+//        XOR-swizzled by row; the B operand is four 4-byte LDS reads from the swizzled segments
+//        (the reads of 8 distinct rows hit distinct banks);
+//      - XR == 1 (M == 1): one 4-byte load per pair in which each lane picks the dword it
+//        fetches so that the row lands already in B-operand order (16-byte unit 8cc + 4h + kb
+//        holds dwords 16h + 4c + kb of chunk cc); the B operand is one 16-byte LDS read and the
+//        pair moves 256 bytes of x instead of 4 rows' 1 KB.
+//    Either way no cross-lane transpose (VALU) is needed.
+//  * The pair's scales ([chunk][block][16 channels], 64*NBW bytes) ride in the same slot: one
+//    16-byte direct-to-LDS load with 4*NBW active lanes per pair, so no scale traffic sits in
+//    front of the first pair.  Per pair the wave issues NBW + XD + 1 memory instructions
+//    (XD = 1 for XR == 1, XR / 4 otherwise).
 //  * Weight segments are stored transposed (segment (i % 8) + 8*kb of a chunk holds packed lane
 //    4*(i % 8) + kb), so the 16-byte A-operand reads of 8 consecutive lanes are conflict-free.
+//  * The steady-state loop is unrolled by the ring size, so every slot offset is a compile-time
+//    constant carried in the LDS instructions' offset fields; per-lane LDS bases and global
+//    offsets are computed once, the per-pair advance is wave-uniform (scalar registers).
+//    Apart from the dequantisation the loop does almost no vector arithmetic.
 // Dequantisation is dq_frag, bit-identical to the reference's fp16 subtract-then-multiply.
 // Every ring load runs with all 64 lanes active (clamped addresses), so each pair is exactly
 // OPS vector-memory instructions and the vmcnt arithmetic is exact.
-template <int NBW, int WAVES, int D, int XD>
+template <int NBW, int WAVES, int D, int XR>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
@@ -464,22 +477,30 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                    int M, int N, int K, int gshift, int splits, int kcw) {
     constexpr int S = D + 1;                                 // ring slots
     constexpr int WSLOT = NBW * 1024;                        // [n16 block][chunk][32 x 16 B]
-    constexpr int XSLOT = XD * 1024;                         // [4*XD rows][16 x 16 B]
-    constexpr int SLOT = WSLOT + XSLOT;
-    constexpr int SBYTES = 2048;                             // [group][block][16 halves]
-    constexpr int WAVE_BYTES = SBYTES + S * SLOT;
-    constexpr int OPS = NBW + XD;
+    constexpr int XSLOT = XR * 256;                          // [XR rows][16 x 16 B]
+    constexpr int SCOFF = WSLOT + XSLOT;                     // [chunk][block][16 halves]
+    constexpr int SLOT = SCOFF + 64 * NBW;
+    constexpr int WAVE_BYTES = S * SLOT;
+    constexpr int XD = XR == 1 ? 1 : XR / 4;                 // x loads per pair
+    constexpr int OPS = NBW + XD + 1;
     static_assert((D - 1) * OPS <= 63, "too many loads in flight for vmcnt");
     static_assert(WAVES >= NBW && WAVE_BYTES >= NBW * 1024, "reduction layout");
+    static_assert(S * SLOT < 65536, "slot offsets must fit the LDS offset field");
+    static_assert(XR == 1 || XR == 4 || XR == 8 || XR == 16, "x rows per slot");
     __shared__ __attribute__((aligned(16))) char wl[WAVES * WAVE_BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kb = lane >> 4;
     const int li = lane & 15;
-    const int split = blockIdx.x % splits;
-    const int tile = blockIdx.x / splits;
+    // Workgroups are dealt to the 8 XCDs round-robin (b % 8).  Give each XCD a contiguous range of
+    // (tile, split) indices, so that neighbouring column tiles -- which share the 128-byte lines
+    // of every scale row -- meet in one L2.  A bijection: the results do not depend on it.
+    const int nwg = gridDim.x;
+    const int bid = (nwg & 7) == 0 ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int split = bid % splits;
+    const int tile = bid / splits;
     const int KC = K >> 6;
     const int kc0 = (split * WAVES + wave) * kcw;
     const int nb0 = tile * NBW;
@@ -487,78 +508,106 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     char* wreg = wl + wave * WAVE_BYTES;
     const uint32_t lds_wave = (uint32_t)reinterpret_cast<uintptr_t>(wreg);
 
-    // Scales of groups g0 .. g0 + ng - 1: lane j of load q fills [group][block][half] entry
-    // e = 64q + j (8 channels), clamped to the last real entry.
-    {
-        const int g0 = kc0 >> gshift;
-        const int last = (kcw >> gshift) * NBW * 2 - 1;
+    // Ring load sources: a base that advances per pair plus a fixed per-lane byte offset.
+    // Weights: lane j fills segment j & 31 of chunk j >> 5 with packed lane 4*(seg % 8) + seg / 8.
+    // x, XR >= 4: lane j of load q fills row r = (64q + j) / 16, segment j % 16, with global
+    // segment (j % 16) ^ (r % 8) of row min(r, M - 1).  x, XR == 1: lane j fills dword j of the
+    // row's 256 bytes, i.e. dword e = j % 4 of unit u = j / 4 (chunk u / 8, half (u / 4) % 2,
+    // lane group u % 4), so it fetches dword 32*(u/8) + 16*((u/4)%2) + 4e + u%4 of the row's pair.
+    const int wseg = lane & 31;
+    const uint32_t woff_g = (uint32_t)((((lane >> 5) * 32) + 4 * (wseg & 7) + (wseg >> 3)) * 16);
+    const char* wbase_g = reinterpret_cast<const char*>(Wp) + ((size_t)nb0 * KC + kc0) * 512;
+    // Scales: lane e < 4*NBW fills entry e = [chunk cc][block b][half] (8 channels) with the
+    // scales of chunk kc0 + 2p + cc; the group advances by 2 >> gshift per pair.
+    const int se = min(lane, 4 * NBW - 1);
+    const char* ssrc = reinterpret_cast<const char*>(
+        scales + (size_t)((kc0 + se / (2 * NBW)) >> gshift) * N + (size_t)(nb0 + (se >> 1) % NBW) * 16 + (se & 1) * 8);
+    const size_t sstep = (size_t)(2 >> gshift) * N * 2;      // bytes per pair
+    const char* xsrc[XD];
+    if constexpr (XR == 1) {
+        const int u = lane >> 2;
+        xsrc[0] = reinterpret_cast<const char*>(x) + (size_t)kc0 * 128 +
+                  (32 * (u >> 3) + 16 * ((u >> 2) & 1) + 4 * (lane & 3) + (u & 3)) * 4;
+    } else {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int e = min(64 * q + lane, last);
-            const uint16_t* src = scales + (size_t)(g0 + e / (2 * NBW)) * N + (size_t)(nb0 + (e >> 1) % NBW) * 16 + (e & 1) * 8;
-            __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(wreg + q * 1024),
-                                             16, 0, 0);
+        for (int q = 0; q < XD; ++q) {
+            const int r = (64 * q + lane) >> 4;
+            const int gseg = (lane & 15) ^ (r & 7);
+            xsrc[q] = reinterpret_cast<const char*>(x + (size_t)min(r, M - 1) * K + (size_t)kc0 * 64 + gseg * 8);
         }
     }
-
-    // Per-lane sources of the ring loads.  Weights: lane j fills segment j & 31 of chunk j >> 5
-    // with packed lane 4*(seg % 8) + seg / 8.  x: lane j of load q fills row r = (64q + j) / 16,
-    // segment j % 16, with global segment (j % 16) ^ (r % 8) of row min(r, M - 1).
-    const int wseg = lane & 31;
-    const u4* wsrc = Wp + ((size_t)nb0 * KC + kc0 + (lane >> 5)) * 32 + 4 * (wseg & 7) + (wseg >> 3);
-    const uint16_t* xsrc[XD];
-#pragma unroll
-    for (int q = 0; q < XD; ++q) {
-        const int r = (64 * q + lane) >> 4;
-        const int gseg = (lane & 15) ^ (r & 7);
-        xsrc[q] = x + (size_t)min(r, M - 1) * K + (size_t)kc0 * 64 + gseg * 8;
-    }
-    auto issue = [&](int p, int s) {
-        char* sl = wreg + SBYTES + s * SLOT;
+    auto issue = [&](int p, auto slot) {
+        char* sl = wreg + decltype(slot)::value * SLOT;
 #pragma unroll
         for (int b = 0; b < NBW; ++b)
-            __builtin_amdgcn_global_load_lds((const void*)(wsrc + (size_t)b * KC * 32 + (size_t)p * 64),
+            __builtin_amdgcn_global_load_lds((const void*)(wbase_g + (size_t)b * KC * 512 + (size_t)p * 1024 + woff_g),
                                              (__attribute__((address_space(3))) void*)(sl + b * 1024), 16, 0, 0);
+        if constexpr (XR == 1) {
+            __builtin_amdgcn_global_load_lds((const void*)(xsrc[0] + (size_t)p * 256),
+                                             (__attribute__((address_space(3))) void*)(sl + WSLOT), 4, 0, 0);
+        } else {
 #pragma unroll
-        for (int q = 0; q < XD; ++q)
-            __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * 128),
-                                             (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024), 16, 0, 0);
+            for (int q = 0; q < XD; ++q)
+                __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * 256),
+                                                 (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024), 16, 0, 0);
+        }
+        if (lane < 4 * NBW)
+            __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)p * sstep),
+                                             (__attribute__((address_space(3))) void*)(sl + SCOFF), 16, 0, 0);
         asm volatile("" ::: "memory");
     };
 
-    // Per-lane LDS read offsets.
+    // Per-lane LDS bases (slot 0).  x, XR >= 4: global segment 8*cc + 4*h + c of row xr sits at
+    // position 8*cc + ((4*h + c) ^ (xr % 8)); lane (kb, j) reads dword kb of it.  x, XR == 1:
+    // lane (kb, j) reads unit 8*cc + 4*h + kb.  Weights: segment (li % 8) + 8*kb.  Scales:
+    // channel li of [group][block].
     const int xr = min(li, M - 1);
-    uint32_t xoff[2][2];
+    uint32_t xb[2][XR == 1 ? 1 : 4];
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
+    for (int h = 0; h < 2; ++h) {
+        if constexpr (XR == 1) {
+            xb[h][0] = lds_wave + WSLOT + ((4 * h + kb) << 4);
+        } else {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) xoff[cc][h] = WSLOT + xr * 256 + (((cc * 8 + 4 * h + kb) ^ (xr & 7)) << 4);
-    const uint32_t woff = ((li & 7) + 8 * kb) << 4;
-    const uint32_t soff = lds_wave + li * 2;
+            for (int c = 0; c < 4; ++c)
+                xb[h][c] = lds_wave + WSLOT + xr * 256 + (((4 * h + c) ^ (xr & 7)) << 4) + 4 * kb;
+        }
+    }
+    const uint32_t wb = lds_wave + (((li & 7) + 8 * kb) << 4);
+    const uint32_t sb = lds_wave + SCOFF + li * 2;
     const Dq d = dq_setup(lane);
 
     f4 acc[NBW];
 #pragma unroll
     for (int b = 0; b < NBW; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // Pair p sits in slot s; its loads (and the scale loads, which are older) are complete.
-    auto consume = [&](int p, int s) {
-        const uint32_t base = lds_wave + SBYTES + s * SLOT;
+    // Pair p sits in ring slot `slot` (a compile-time constant); its loads (and the scale loads,
+    // which are older) are complete.
+    auto consume = [&](int p, auto slot) {
+        constexpr int SO = decltype(slot)::value * SLOT;
         u4 xv[2][2], wv[2][NBW];
         uint32_t sc[2][NBW];
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) xv[cc][h] = lds_read_u4(base + xoff[cc][h]);
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int b = 0; b < NBW; ++b) wv[cc][b] = lds_read_u4(base + b * 1024 + cc * 512 + woff);
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int b = 0; b < NBW; ++b)
-                sc[cc][b] = lds_read_u16(soff + ((((2 * p + cc) >> gshift) * NBW + b) << 5));
+        static_for<0, 2>([&](auto cc) {
+            static_for<0, 2>([&](auto h) {
+                constexpr int O = SO + decltype(cc)::value * 128;
+                constexpr int H = decltype(h)::value;
+                if constexpr (XR == 1) {
+                    xv[cc][h] = lds_read_u4_at<O>(xb[H][0]);
+                } else {
+                    xv[cc][h] = u4{lds_read_u32_at<O>(xb[H][0]), lds_read_u32_at<O>(xb[H][1]),
+                                   lds_read_u32_at<O>(xb[H][2]), lds_read_u32_at<O>(xb[H][3])};
+                }
+            });
+        });
+        static_for<0, 2>([&](auto cc) {
+            static_for<0, NBW>([&](auto b) {
+                wv[cc][b] = lds_read_u4_at<SO + decltype(b)::value * 1024 + decltype(cc)::value * 512>(wb);
+            });
+        });
+        static_for<0, NBW>([&](auto b) {
+            sc[0][b] = lds_read_u16_at<SO + decltype(b)::value * 32>(sb);
+            sc[1][b] = lds_read_u16_at<SO + (NBW + decltype(b)::value) * 32>(sb);
+        });
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
@@ -569,8 +618,9 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         }
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            const h8 b0 = __builtin_bit_cast(h8, xpose_rows(xv[cc][0]));
-            const h8 b1 = __builtin_bit_cast(h8, xpose_rows(xv[cc][1]));
+            const u4 x0 = xv[cc][0], x1 = xv[cc][1];
+            const h8 b0 = __builtin_bit_cast(h8, x0);
+            const h8 b1 = __builtin_bit_cast(h8, x1);
 #pragma unroll
             for (int b = 0; b < NBW; ++b) {
                 const h2 s2 = scale2((uint16_t)sc[cc][b]);
@@ -582,26 +632,34 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     };
 
     // Prologue: pairs 0..D-1 in slots 0..D-1 (npair >= D, checked by the planner).  Steady
-    // state: wait for pair p (D-1 younger pairs may stay in flight), refill with pair p + D, then
-    // compute pair p.  Drain: the last D pairs with shrinking waits.  The scale loads are older
-    // than pair 0, so the first wait covers them too.
-#pragma unroll
-    for (int s = 0; s < D; ++s) issue(s, s);
-    int sc_ = 0, si = D;                                     // slot of pair p, slot for pair p + D
+    // state, S pairs per iteration: wait for pair p (D-1 younger pairs may stay in flight), refill
+    // with pair p + D, then compute pair p; pair p lives in slot p % S.  Tail: the remaining
+    // (< S) steady steps, then the last D pairs with shrinking waits.
+    static_for<0, D>([&](auto s) { issue(s, s); });
+    const int nsteady = npair - D;
     int p = 0;
-    for (; p + D < npair; ++p) {
-        wait_vmcnt((D - 1) * OPS);
-        issue(p + D, si);
-        consume(p, sc_);
-        sc_ = sc_ + 1 == S ? 0 : sc_ + 1;
-        si = si + 1 == S ? 0 : si + 1;
+    for (; p + S <= nsteady; p += S) {
+        static_for<0, S>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            wait_vmcnt((D - 1) * OPS);
+            issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
+            consume(p + T, t);
+        });
     }
-#pragma unroll
-    for (int t = 0; t < D; ++t) {
-        wait_vmcnt((D - 1 - t) * OPS);
-        consume(p + t, sc_);
-        sc_ = sc_ + 1 == S ? 0 : sc_ + 1;
-    }
+    static_switch<0, S>(nsteady - p, [&](auto r) {
+        constexpr int R = decltype(r)::value;
+        static_for<0, R>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            wait_vmcnt((D - 1) * OPS);
+            issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
+            consume(p + T, t);
+        });
+        static_for<0, D>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            wait_vmcnt((D - 1 - T) * OPS);
+            consume(p + R + T, std::integral_constant<int, (R + T) % S>{});
+        });
+    });
 
     // Cross-wave reduction in wave order; each wave parks its tile at the start of its region
     // (its own loads are complete and its LDS reads have returned).
@@ -1117,17 +1175,19 @@ static hipError_t launch_decode_v(const w4a16_plan& p, const u4* Wp, const uint1
         hipLaunchKernelGGL((decode_stream_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
                            Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
     } else if constexpr (c.kind == 3) {
-        const int xd = decode_ring_xd(p.M);
-#define W4A16_RING(XD)                                                                                   \
-        hipLaunchKernelGGL((decode_ring_kernel<c.nbw, c.waves, c.d, XD>), dim3(p.grid), dim3(c.waves * 64), \
+        const int xr = decode_ring_xr(p.M);
+#define W4A16_RING(XR)                                                                                   \
+        hipLaunchKernelGGL((decode_ring_kernel<c.nbw, c.waves, c.d, XR>), dim3(p.grid), dim3(c.waves * 64), \
                            0, st, Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks)
-        // Shapes whose ring does not fit in LDS for 8 or 16 token rows are never planned for them.
-        if (xd == 1) {
-            W4A16_RING(1);
-        } else if (xd == 2) {
-            if constexpr (decode_lds_bytes(V, 8) <= 163840) W4A16_RING(2); else return hipErrorInvalidValue;
+        // Shapes whose ring does not fit in LDS for a row count are never planned for it.
+        if (xr == 1) {
+            if constexpr (decode_lds_bytes(V, 1) <= 163840) W4A16_RING(1); else return hipErrorInvalidValue;
+        } else if (xr == 4) {
+            if constexpr (decode_lds_bytes(V, 4) <= 163840) W4A16_RING(4); else return hipErrorInvalidValue;
+        } else if (xr == 8) {
+            if constexpr (decode_lds_bytes(V, 8) <= 163840) W4A16_RING(8); else return hipErrorInvalidValue;
         } else {
-            if constexpr (decode_lds_bytes(V, 16) <= 163840) W4A16_RING(4); else return hipErrorInvalidValue;
+            if constexpr (decode_lds_bytes(V, 16) <= 163840) W4A16_RING(16); else return hipErrorInvalidValue;
         }
 #undef W4A16_RING
     } else {
@@ -1149,6 +1209,8 @@ static hipError_t launch_decode(const w4a16_plan& p, const u4* Wp, const uint16_
         W4A16_DEC_CASE(20) W4A16_DEC_CASE(21) W4A16_DEC_CASE(22) W4A16_DEC_CASE(23)
         W4A16_DEC_CASE(24) W4A16_DEC_CASE(25) W4A16_DEC_CASE(26) W4A16_DEC_CASE(27)
         W4A16_DEC_CASE(28) W4A16_DEC_CASE(29) W4A16_DEC_CASE(30) W4A16_DEC_CASE(31)
+        W4A16_DEC_CASE(32) W4A16_DEC_CASE(33) W4A16_DEC_CASE(34) W4A16_DEC_CASE(35)
+        W4A16_DEC_CASE(36) W4A16_DEC_CASE(37) W4A16_DEC_CASE(38) W4A16_DEC_CASE(39)
 #undef W4A16_DEC_CASE
         default: return hipErrorInvalidValue;
     }

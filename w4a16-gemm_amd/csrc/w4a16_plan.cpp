@@ -185,10 +185,12 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
         if (var < 0) {
             // Shapes measured fastest on MI355X (graph-timed sweep over the whole table) for the
             // Llama-3 decode projections, tried in order; the first that fits wins:
-            //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): streaming ring
-            //    of 4 blocks x 4 waves, no split;
-            //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves
-            //    (two-block tiles split in two at M > 8, where x traffic per block grows);
+            //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): a refill-ahead
+            //    ring of 2 blocks x 4 waves while the x rows are few (M <= 4), else the streaming
+            //    ring of 4 blocks x 4 waves; no split;
+            //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves,
+            //    3 pairs in flight for one token row and 2 up to 8 rows (two-block tiles split in
+            //    two above 8 rows, where the x traffic per block grows);
             //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves.
             auto ok = [&](int cand, int sp) {
                 return decode_shape_fits(cand, KC, sp, G) && decode_lds_bytes(cand, M) <= lim->lds_bytes_per_block &&
@@ -196,16 +198,18 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             };
             auto ntiles_of = [&](int cand) { return N / (16 * kDecodeTable[cand].nbw); };
             struct Cand { int v, sp; };
-            Cand wide[] = {{20, 1}, {7, 1}};
-            Cand longk_small_m[] = {{27, 1}, {30, 2}};
-            Cand longk_large_m[] = {{30, 2}, {27, 1}};
-            Cand shortk_m4[] = {{22, 1}, {27, 1}};
-            Cand shortk[] = {{27, 1}, {29, 1}};
+            Cand wide_small_m[] = {{28, 1}, {20, 1}, {7, 1}};
+            Cand wide[] = {{20, 1}, {7, 1}, {7, 1}};
+            Cand longk_m1[] = {{37, 1}, {27, 1}, {30, 2}};
+            Cand longk_small_m[] = {{27, 1}, {30, 2}, {30, 2}};
+            Cand longk_large_m[] = {{30, 2}, {27, 1}, {27, 1}};
+            Cand shortk_m1[] = {{37, 1}, {27, 1}, {22, 1}};
+            Cand shortk[] = {{27, 1}, {29, 1}, {29, 1}};
             Cand* list;
-            int n;
-            if ((int64_t)ntiles_of(20) * 8 >= 7LL * cus) { list = wide; n = 2; }
-            else if (KC >= 128) { list = M <= 8 ? longk_small_m : longk_large_m; n = 2; }
-            else { list = M <= 4 ? shortk_m4 : shortk; n = 2; }
+            const int n = 3;
+            if ((int64_t)ntiles_of(20) * 8 >= 7LL * cus) list = M <= 4 ? wide_small_m : wide;
+            else if (KC >= 128) list = M <= 1 ? longk_m1 : M <= 8 ? longk_small_m : longk_large_m;
+            else list = M <= 1 ? shortk_m1 : shortk;
             for (int i = 0; i < n && var < 0; ++i)
                 if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus) {
                     var = list[i].v; splits = list[i].sp;

@@ -4,9 +4,11 @@
 Counterpart of the reference's benchmarks/measure_bw.py (same method: best of 30 timed runs of a
 device copy and of a read-only pass, bandwidth = bytes moved / time), sized for MI355X: the
 default buffer is 1 GiB, four times the 256 MB Infinity Cache (the reference's 256 MiB default
-would be cache-resident here).  The read-only pass is a streaming-read kernel (csrc/bw_probe.hip,
-built into libw4a16_bwprobe.so by build.py): torch's reductions on this GPU run far below the
-memory rate, so they would measure the reduction kernel, not the memory.  It also measures the per-launch rate at the size of one
+would be cache-resident here).  The copy is measured twice, with torch's copy_ (the reference's
+method) and with a one-shot copy kernel; the read-only pass is a one-shot streaming-read kernel
+(both in csrc/bw_probe.hip, built into libw4a16_bwprobe.so by build.py): torch's reductions on
+this GPU run far below the memory rate, so they would measure the reduction kernel, not the
+memory.  It also measures the per-launch rate at the size of one
 decode call (30 MiB) the way bench.py times the op: a HIP graph of launches over buffer copies
 whose working set exceeds the Infinity Cache, so every launch streams from HBM and pays its
 launch cost.
@@ -31,8 +33,10 @@ def load_probe():
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built (python w4a16-gemm_amd/build.py)")
     lib = ctypes.CDLL(path)
-    lib.w4a16_bw_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.w4a16_bw_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
     lib.w4a16_bw_read.restype = ctypes.c_int
+    lib.w4a16_bw_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.w4a16_bw_copy.restype = ctypes.c_int
     return lib
 
 
@@ -88,17 +92,23 @@ def main(argv=None) -> int:
     n = a.mb * 2**20
     src = torch.empty(n, dtype=torch.uint8, device="cuda").random_()
     dst = torch.empty_like(src)
-    blocks = 8 * torch.cuda.get_device_properties(0).multi_processor_count
-    sink = torch.empty(blocks, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
 
     def read(buf, nbytes):
-        rc = probe.w4a16_bw_read(buf.data_ptr(), nbytes, sink.data_ptr(), blocks,
-                                 torch.cuda.current_stream().cuda_stream)
+        rc = probe.w4a16_bw_read(buf.data_ptr(), nbytes, sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
         if rc:
             raise RuntimeError(f"w4a16_bw_read failed ({rc})")
 
+    def copy(s, d, nbytes):
+        rc = probe.w4a16_bw_copy(s.data_ptr(), d.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"w4a16_bw_copy failed ({rc})")
+
     out = {"gpu": torch.cuda.get_device_name(), "buffer_mib": a.mb}
-    out["copy_gbs"] = 2 * n / best_ms(torch, lambda: dst.copy_(src)) / 1e6
+    out["copy_torch_gbs"] = 2 * n / best_ms(torch, lambda: dst.copy_(src)) / 1e6
+    out["copy_gbs"] = 2 * n / best_ms(torch, lambda: copy(src, dst, n)) / 1e6
+    if not torch.equal(src, dst):
+        raise RuntimeError("w4a16_bw_copy produced a wrong copy")
     out["read_gbs"] = n / best_ms(torch, lambda: read(src, n)) / 1e6
     del dst
     # Per-launch read rate at one call's size: distinct slices of the big buffer (>= 2x the MALL).
@@ -109,7 +119,8 @@ def main(argv=None) -> int:
     out.update({"call_mib": a.call_mb, "call_copies": copies, "call_median_us": med, "call_min_us": mn,
                 "call_read_gbs": m / (med * 1e-6) / 1e9})
     print(out["gpu"])
-    print(f"copy (read+write) : {out['copy_gbs']:8.1f} GB/s   ({a.mb} MiB buffers)")
+    print(f"copy (read+write) : {out['copy_gbs']:8.1f} GB/s   ({a.mb} MiB buffers; torch copy_: "
+          f"{out['copy_torch_gbs']:.1f} GB/s)")
     print(f"read (read only)  : {out['read_gbs']:8.1f} GB/s")
     print(f"per-launch read   : {out['call_read_gbs']:8.1f} GB/s   ({a.call_mb:g} MiB per launch, {copies} buffers "
           f"in a graph: median {med:.2f} us, min {mn:.2f} us per launch)")
