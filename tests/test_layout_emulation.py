@@ -335,8 +335,8 @@ def test_wide_prefill_addresses_in_bounds(cfg, M, N, K, G):
                 assert m0 * K * 2 + (KC - 1) * 128 + xoff + 16 <= sizes["x"]
 
 
-def ring_x_rows(x, M, K, kc0, p, XR):
-    """decode_ring_kernel x rows of pair p as they land in LDS: XR rows x 64 dwords (each dword a
+def ring_x_rows(x, M, K, c0, XR):
+    """decode_ring_kernel x rows of the chunk pair starting at chunk c0 as they land in LDS: XR rows x 64 dwords (each dword a
     pair of fp64 halves).  XR == 1: one 4-byte load, lane j fetching dword 32*(u/8) + 16*((u/4)%2)
     + 4*(j%4) + u%4 of the pair (u = j / 4).  XR >= 4: 16-byte loads of 4 rows each, lane j of
     load q filling row (64q + j) / 16, segment j % 16 with global segment (j % 16) ^ (row % 8).
@@ -347,7 +347,7 @@ def ring_x_rows(x, M, K, kc0, p, XR):
         for lane in range(64):
             u = lane >> 2
             d = 32 * (u >> 3) + 16 * ((u >> 2) & 1) + 4 * (lane & 3) + (u & 3)
-            off = kc0 * 128 + p * 256 + 4 * d
+            off = c0 * 128 + 4 * d
             hi = max(hi, off + 4)
             slot[0, lane] = x[0, off // 2:off // 2 + 2]
         return slot, hi
@@ -355,7 +355,7 @@ def ring_x_rows(x, M, K, kc0, p, XR):
         for lane in range(64):
             r = (64 * q + lane) >> 4
             gseg = (lane & 15) ^ (r & 7)
-            off = kc0 * 128 + p * 256 + gseg * 16
+            off = c0 * 128 + gseg * 16
             hi = max(hi, off + 16)
             for e in range(4):
                 slot[r, 4 * (lane & 15) + e] = x[min(r, M - 1), off // 2 + 2 * e:off // 2 + 2 * e + 2]
@@ -391,7 +391,8 @@ def ring_b_operand(slot, M, XR, cc, h):
 ])
 def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
     """decode_ring_kernel x paths (4-byte loads in B-operand order for M = 1, swizzled 16-byte
-    loads plus four 4-byte LDS reads otherwise) with the weights as in decode_kernel: the emulated
+    loads plus four 4-byte LDS reads otherwise), the waves of a workgroup interleaved over K (wave w
+    takes chunk pairs w, w + WAVES, ...), the weights as in decode_kernel: the emulated
     result equals the float64 matmul, every x source offset stays inside the row, every B operand
     holds x[row][32h + 8c + 2kb + {0,1}] in slot pair c, and the first-dword reads of 8 consecutive
     lanes with 8 distinct rows hit 8 distinct 16-byte bank groups."""
@@ -409,10 +410,11 @@ def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
         fin = np.zeros((NBW, 64, 4))
         for split in range(splits):
             for wave in range(WAVES):
-                kc0 = (split * WAVES + wave) * kcw
+                kc0 = split * WAVES * kcw + 2 * wave
                 acc = np.zeros((NBW, 64, 4))
                 for p in range(kcw // 2):
-                    slot, hi = ring_x_rows(x, M, K, kc0, p, XR)
+                    c0 = kc0 + 2 * WAVES * p
+                    slot, hi = ring_x_rows(x, M, K, c0, XR)
                     assert hi <= 2 * K
                     for cc in range(2):
                         Bs = []
@@ -420,7 +422,7 @@ def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
                             B, addr = ring_b_operand(slot, M, XR, cc, h)
                             for lane in range(64):
                                 kb, j = lane >> 4, lane & 15
-                                base = (kc0 + 2 * p + cc) * 64 + 32 * h + 2 * kb
+                                base = (c0 + cc) * 64 + 32 * h + 2 * kb
                                 want = [x[min(j, M - 1), base + 8 * c + e] for c in range(4) for e in range(2)]
                                 assert np.array_equal(B[lane], want)
                             for g0 in range(0, 64, 8):
@@ -428,7 +430,7 @@ def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
                                 if len(rows) == 8:
                                     assert len({a // 16 % 8 for a in addr[g0:g0 + 8]}) == 8
                             Bs.append(B)
-                        kc = kc0 + 2 * p + cc
+                        kc = c0 + cc
                         for b in range(NBW):
                             nb = tile * NBW + b
                             Sn = s[kc * 64 // G, nb * 16:nb * 16 + 16]

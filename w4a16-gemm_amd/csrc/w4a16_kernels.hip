@@ -502,7 +502,11 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int split = bid % splits;
     const int tile = bid / splits;
     const int KC = K >> 6;
-    const int kc0 = (split * WAVES + wave) * kcw;
+    // The workgroup's waves interleave over its K range: wave w takes chunk pairs w, w + WAVES,
+    // w + 2*WAVES, ..., so each step of the ring reads 1 KB x WAVES of contiguous weights per
+    // block (measured faster than a contiguous range per wave, whose waves stream 1 KB pieces
+    // of separate regions).
+    const int kc0 = split * WAVES * kcw + 2 * wave;
     const int nb0 = tile * NBW;
     const int npair = kcw >> 1;
     char* wreg = wl + wave * WAVE_BYTES;
@@ -518,11 +522,11 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const uint32_t woff_g = (uint32_t)((((lane >> 5) * 32) + 4 * (wseg & 7) + (wseg >> 3)) * 16);
     const char* wbase_g = reinterpret_cast<const char*>(Wp) + ((size_t)nb0 * KC + kc0) * 512;
     // Scales: lane e < 4*NBW fills entry e = [chunk cc][block b][half] (8 channels) with the
-    // scales of chunk kc0 + 2p + cc; the group advances by 2 >> gshift per pair.
+    // scales of chunk kc0 + 2*WAVES*p + cc; the group advances by WAVES * (2 >> gshift) per pair.
     const int se = min(lane, 4 * NBW - 1);
     const char* ssrc = reinterpret_cast<const char*>(
         scales + (size_t)((kc0 + se / (2 * NBW)) >> gshift) * N + (size_t)(nb0 + (se >> 1) % NBW) * 16 + (se & 1) * 8);
-    const size_t sstep = (size_t)(2 >> gshift) * N * 2;      // bytes per pair
+    const size_t sstep = (size_t)(2 >> gshift) * N * 2;      // bytes per chunk pair
     const char* xsrc[XD];
     if constexpr (XR == 1) {
         const int u = lane >> 2;
@@ -540,19 +544,19 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         char* sl = wreg + decltype(slot)::value * SLOT;
 #pragma unroll
         for (int b = 0; b < NBW; ++b)
-            __builtin_amdgcn_global_load_lds((const void*)(wbase_g + (size_t)b * KC * 512 + (size_t)p * 1024 + woff_g),
+            __builtin_amdgcn_global_load_lds((const void*)(wbase_g + (size_t)b * KC * 512 + (size_t)p * (1024 * WAVES) + woff_g),
                                              (__attribute__((address_space(3))) void*)(sl + b * 1024), 16, 0, 0);
         if constexpr (XR == 1) {
-            __builtin_amdgcn_global_load_lds((const void*)(xsrc[0] + (size_t)p * 256),
+            __builtin_amdgcn_global_load_lds((const void*)(xsrc[0] + (size_t)p * (256 * WAVES)),
                                              (__attribute__((address_space(3))) void*)(sl + WSLOT), 4, 0, 0);
         } else {
 #pragma unroll
             for (int q = 0; q < XD; ++q)
-                __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * 256),
+                __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * (256 * WAVES)),
                                                  (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024), 16, 0, 0);
         }
         if (lane < 4 * NBW)
-            __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)p * sstep),
+            __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)p * (sstep * WAVES)),
                                              (__attribute__((address_space(3))) void*)(sl + SCOFF), 16, 0, 0);
         asm volatile("" ::: "memory");
     };

@@ -185,11 +185,11 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
         if (var < 0) {
             // Shapes measured fastest on MI355X (graph-timed sweep over the whole table) for the
             // Llama-3 decode projections, tried in order; the first that fits wins:
-            //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): a refill-ahead
-            //    ring of 2 blocks x 4 waves while the x rows are few (M <= 4), else the streaming
-            //    ring of 4 blocks x 4 waves; no split;
+            //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): refill-ahead
+            //    rings of 4 waves, 2 blocks while the x rows are few (M <= 4), else 4 blocks; no
+            //    split;
             //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves,
-            //    3 pairs in flight for one token row and 2 up to 8 rows (two-block tiles split in
+            //    3 pairs in flight up to 4 token rows and 2 up to 8 rows (two-block tiles split in
             //    two above 8 rows, where the x traffic per block grows);
             //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves.
             auto ok = [&](int cand, int sp) {
@@ -199,8 +199,8 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             auto ntiles_of = [&](int cand) { return N / (16 * kDecodeTable[cand].nbw); };
             struct Cand { int v, sp; };
             Cand wide_small_m[] = {{28, 1}, {20, 1}, {7, 1}};
-            Cand wide[] = {{20, 1}, {7, 1}, {7, 1}};
-            Cand longk_m1[] = {{37, 1}, {27, 1}, {30, 2}};
+            Cand wide[] = {{24, 1}, {20, 1}, {7, 1}};
+            Cand longk_m4[] = {{37, 1}, {27, 1}, {30, 2}};
             Cand longk_small_m[] = {{27, 1}, {30, 2}, {30, 2}};
             Cand longk_large_m[] = {{30, 2}, {27, 1}, {27, 1}};
             Cand shortk_m1[] = {{37, 1}, {27, 1}, {22, 1}};
@@ -208,7 +208,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             Cand* list;
             const int n = 3;
             if ((int64_t)ntiles_of(20) * 8 >= 7LL * cus) list = M <= 4 ? wide_small_m : wide;
-            else if (KC >= 128) list = M <= 1 ? longk_m1 : M <= 8 ? longk_small_m : longk_large_m;
+            else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
             else list = M <= 1 ? shortk_m1 : shortk;
             for (int i = 0; i < n && var < 0; ++i)
                 if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus) {
