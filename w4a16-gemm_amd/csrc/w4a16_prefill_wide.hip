@@ -41,8 +41,18 @@ namespace w4a16 {
 //  * XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so block b is
 //    given tile (b % 8) * (G / 8) + b / 8: each XCD walks consecutive tiles, i.e. the M tiles
 //    that share a weight tile, through its own L2.
+// Waves per SIMD the wide kernels are compiled for.  128 x 256 tiles (1 x 4 waves): 2, i.e. two
+// workgroups per CU, so one workgroup's MFMAs run while the other dequantises, stages x and
+// waits at its barrier (at 1, the default for its 328 registers, the matrix cores idled ~48% of
+// the time).  The compiler then keeps the 128 accumulators in VGPRs and spills three registers
+// outside the loop.  The other shapes stay at 1: at 2, 256 x 128 spills 67 times inside its loop
+// and 128 x 128 spills a pending asm-load destination (tests/test_isa_hazards.py rejects that).
+template <int WAVES_M, int WAVES_N>
+constexpr int kWideWavesPerEu = WAVES_M == 1 && WAVES_N == 4 ? 2 : 1;
+
 template <int BM, int BN, int WAVES_M, int WAVES_N>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
+__attribute__((amdgpu_waves_per_eu(kWideWavesPerEu<WAVES_M, WAVES_N>, kWideWavesPerEu<WAVES_M, WAVES_N>)))
 prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
                     int M, int N, int K, int gshift, int tiles_m) {
@@ -232,16 +242,22 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         bind_after_wait(w1[q][0]); bind_after_wait(w1[q][1]); bind_after_wait(s1[q]);
     }
 
+    // The lane id again, from v_mbcnt (opaque to the compiler): keeping r and kg live across the
+    // loop would cost two registers, which at two waves per SIMD the allocator spills.
+    int lane_e;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+    const int r_e = lane_e & 31;
+    const int kg_e = lane_e >> 5;
 #pragma unroll
     for (int p = 0; p < TM; ++p) {
-        const int m = m0 + wm * WM + p * 32 + r;
+        const int m = m0 + wm * WM + p * 32 + r_e;
         if (m >= M) continue;
 #pragma unroll
         for (int q = 0; q < TN; ++q) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int nbk = nb0 + 2 * q + (g >> 1);
-                const int n = (nb0 + 2 * q) * 16 + 8 * g + 4 * kg;
+                const int n = (nb0 + 2 * q) * 16 + 8 * g + 4 * kg_e;
                 if (nbk < NBLK)
                     *reinterpret_cast<u2*>(y + (size_t)m * N + n) =
                         pack_f16x4(f4{acc[p][q][4 * g], acc[p][q][4 * g + 1], acc[p][q][4 * g + 2], acc[p][q][4 * g + 3]});
