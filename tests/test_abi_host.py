@@ -170,7 +170,7 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
     (2048, 14336, 4096, 7),                                                  # partial last round: 128x128
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
-    (17, 4096, 14336, 8), (32, 14336, 4096, 8),                              # few token rows, few blocks
+    (17, 4096, 14336, 8), (32, 6144, 4096, 8), (32, 14336, 4096, 10),       # few token rows, few blocks
     (33, 4096, 4096, 10), (64, 4096, 4096, 10), (128, 4096, 14336, 10),      # token groups of 32
     (32, 28672, 4096, 10), (48, 14336, 4096, 10),
     (128, 14336, 4096, 11), (512, 4096, 4096, 11),                           # token groups of 64

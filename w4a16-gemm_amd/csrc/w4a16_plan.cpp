@@ -82,8 +82,9 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     };
     // Rules measured on MI355X (graph-timed sweep of every config over M = 17..1024 on the
     // Llama-3-8B projection shapes):
-    //  * M <= 32 while N/16 blocks are at most 4x the CU count: one wave per n16 block over the
-    //    whole K (prefill_stream_kernel; K = 14336, N = 4096: 52 vs 155 us for 16 x 128 tiles);
+    //  * M <= 32 while N/16 blocks are at most 2x the CU count: one wave per n16 block over the
+    //    whole K (prefill_stream_kernel; K = 14336, N = 4096: 52 vs 155 us for 16 x 128 tiles and
+    //    64 us for token groups; at N = 14336, 896 blocks, token groups win: 21 vs 35 us);
     //  * token groups of 32 rows, 4 waves sharing x (prefill_group_kernel), while the waves
     //    (M/32 groups x N/16 blocks) are at most 12 per CU: e.g. K = 14336, N = 4096, M = 128:
     //    65 vs 152 us; N = 28672, M = 32: 31 vs 49 us;
@@ -92,7 +93,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //  * then the wide tiles, which beat the 16..128-row tiles for every larger size measured
     //    (N = 6144, M = 512: 54 vs 73 us).
     const double blocks = std::ceil(N / 16.0);
-    if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K) && N / 16 <= 4 * lim.cu_count) return 8;
+    if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K) && N / 16 <= 2 * lim.cu_count) return 8;
     if (prefill_occupancy(10, lim) > 0 && prefill_shape_ok(10, M, K) &&
         std::ceil(M / 32.0) * blocks <= 12.0 * cus)
         return 10;
