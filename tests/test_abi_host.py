@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 11
+        assert 1 <= p.kernel <= 15
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -163,7 +163,8 @@ def test_prefill_plan_invariants(lib, M, N):
 
 
 PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128),
-                 8: (32, 16), 9: (64, 16), 10: (32, 64), 11: (64, 64)}
+                 8: (32, 16), 9: (64, 16), 10: (32, 64), 11: (64, 64), 12: (32, 128), 13: (64, 128), 14: (32, 128),
+                 15: (32, 256)}
 
 
 @pytest.mark.parametrize("M,N,K,want", [
@@ -173,8 +174,9 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (17, 4096, 14336, 8), (32, 6144, 4096, 8), (32, 14336, 4096, 10),       # few token rows, few blocks
     (33, 4096, 4096, 10), (64, 4096, 4096, 10), (128, 4096, 14336, 10),      # token groups of 32
     (32, 28672, 4096, 10), (48, 14336, 4096, 10),
-    (128, 14336, 4096, 11), (512, 4096, 4096, 11),                           # token groups of 64
-    (512, 6144, 4096, 7), (128, 28672, 4096, 7),                             # moderate sizes: 128x128 wide
+    (128, 14336, 4096, 14), (512, 4096, 4096, 14), (96, 14336, 4096, 14),    # 2 blocks per wave, 3 pairs
+    (512, 6144, 4096, 12), (192, 14336, 4096, 12),                           # 2 blocks per wave, 2 pairs
+    (256, 14336, 4096, 7), (128, 28672, 4096, 7),                            # moderate sizes: 128x128 wide
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
@@ -185,7 +187,8 @@ def test_prefill_wide_selection(lib, M, N, K, want):
         assert p.kernel == want
     tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
-    assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4}[p.kernel]
+    assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4, 12: 4, 13: 4, 14: 4,
+                            15: 4}[p.kernel]
 
 
 def test_prefill_override(lib, monkeypatch):

@@ -446,3 +446,54 @@ def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
                     y[li, n:n + 4] = fin[b, lane]
     assert not np.isnan(y).any()
     assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-12
+
+
+def group_x_slot(x, M, K, m0, c0, TM):
+    """prefill_group_kernel x rows of one chunk pair (chunks c0, c0+1) as they land in LDS:
+    a dict byte offset -> fp64 half pair (one dword), for TM tiles of 16 token rows.  16-byte
+    direct-to-LDS load q (4 rows) writes rows r0 = 4 (q % 4) .. r0 + 3 of tile t = q // 4 at
+    t * 4352 + r0 * 256 + 128 * (r0 >= 8); lane j writes row r0 + j // 16, position j % 16, with
+    global segment (j % 16) ^ (row % 8) of token min(m0 + 16 t + row, M - 1)."""
+    lds = {}
+    hi = 0
+    for q in range(4 * TM):
+        t, r0 = q // 4, 4 * (q % 4)
+        base = t * 4352 + r0 * 256 + (128 if r0 >= 8 else 0)
+        for lane in range(64):
+            r = r0 + (lane >> 4)
+            g = (lane & 15) ^ (r & 7)
+            off = c0 * 128 + g * 16                         # bytes within the token's row
+            hi = max(hi, off + 16)
+            tok = min(m0 + 16 * t + r, M - 1)
+            for e in range(4):
+                lds[base + lane * 16 + 4 * e] = tuple(x[tok, off // 2 + 2 * e:off // 2 + 2 * e + 2])
+    return lds, hi
+
+
+@pytest.mark.parametrize("M,TM", [(17, 2), (64, 4), (100, 4), (16, 1)])
+def test_group_prefill_x_rows_b_operand(M, TM):
+    """prefill_group_kernel B operands without cross-lane transposes: lane (kb, li) of token tile
+    t, chunk cc, half h reads four dwords at t*4352 + li*256 + 128*(li >= 8) +
+    (8 cc + ((4h + c) ^ (li % 8))) * 16 + 4 kb (c = 0..3); they must hold x[token][32h + 8c + 2kb
+    + {0,1}] of chunk cc, every x source offset stays inside the row, and for every (t, cc, h, c)
+    the 64 lanes hit 64 distinct 4-byte banks (16 distinct rows, no conflicts)."""
+    rng = np.random.default_rng(M)
+    K = 512
+    x = rng.standard_normal((M, K))
+    for m0 in range(0, M, 16 * TM):
+        for c0 in range(0, K // 64, 2):
+            lds, hi = group_x_slot(x, M, K, m0, c0, TM)
+            assert hi <= 2 * K
+            for t in range(TM):
+                for cc in range(2):
+                    for h in range(2):
+                        for c in range(4):
+                            banks = set()
+                            for lane in range(64):
+                                kb, li = lane >> 4, lane & 15
+                                a = t * 4352 + li * 256 + (128 if li >= 8 else 0) + (8 * cc + ((4 * h + c) ^ (li & 7))) * 16 + 4 * kb
+                                banks.add(a // 4 % 64)
+                                tok = min(m0 + 16 * t + li, M - 1)
+                                k = (c0 + cc) * 64 + 32 * h + 8 * c + 2 * kb
+                                assert lds[a] == (x[tok, k], x[tok, k + 1])
+                            assert len(banks) == 64

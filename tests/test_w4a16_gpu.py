@@ -466,9 +466,9 @@ def test_prefill_small_m_bitwise_equal(M, N, K, G):
             assert torch.equal(gemm(Wp, x[:m].contiguous(), scales), y[:m]), m
 
 
-# Token-group prefill (configs 10, 11, forced through W4A16_PREFILL): 4 waves share the x rows of
+# Token-group prefill (configs 10..15, forced through W4A16_PREFILL): 4 waves, 1..4 n16 blocks each, share the x rows of
 # a group of 32 or 64 tokens; any M, N tails (waves past N compute clamped data and store nothing).
-@pytest.mark.parametrize("cfg", [10, 11])
+@pytest.mark.parametrize("cfg", [10, 11, 12, 13, 14, 15])
 @pytest.mark.parametrize("M,N,K,G", [(17, 4096, 4096, 128), (33, 1040, 2048, 64), (100, 272, 1024, 64),
                                      (300, 4112, 4224, 64), (1000, 512, 2048, 128), (64, 16, 1024, 128),
                                      (129, 6144, 4096, 128)])

@@ -16,7 +16,7 @@ namespace w4a16 {
 struct PrefillTile {
     int bm, bn, waves_m, waves_n, kind, depth;
 };
-constexpr PrefillTile kPrefillTable[12] = {
+constexpr PrefillTile kPrefillTable[16] = {
     {0, 0, 0, 0, 0, 0},
     {16, 128, 1, 4, 0, 0},     // 1: small batches: 4 waves across N, wave tile 16 x 32
     {32, 128, 1, 4, 0, 0},     // 2: wave tile 32 x 32
@@ -29,17 +29,29 @@ constexpr PrefillTile kPrefillTable[12] = {
     {64, 16, 1, 1, 2, 3},      // 9: M <= 64, one wave per n16 block, 3 pairs in flight
     {32, 64, 1, 4, 3, 3},      // 10: groups of 32 tokens, 4 n16 blocks per workgroup, 3 pairs
     {64, 64, 1, 4, 3, 2},      // 11: groups of 64 tokens, 4 n16 blocks per workgroup, 2 pairs
+    {32, 128, 1, 4, 3, 2},     // 12: groups of 32 tokens, 2 n16 blocks per wave, 2 pairs
+    {64, 128, 1, 4, 3, 2},     // 13: groups of 64 tokens, 2 n16 blocks per wave, 2 pairs (forced only)
+    {32, 128, 1, 4, 3, 3},     // 14: groups of 32 tokens, 2 n16 blocks per wave, 3 pairs
+    {32, 256, 1, 4, 3, 2},     // 15: groups of 32 tokens, 4 n16 blocks per wave, 2 pairs (forced only)
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 11;     // all prefill configs
+constexpr int kNumPrefillTable = 15;     // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;
 
-// Ring slot of kinds 2 and 3: per wave 1 KB of weights and 1 KB of scales, plus the x rows of the
-// token group (bm rows x 256 B).
+// Bytes of one 16-row token tile in a prefill_group_kernel slot: 16 rows x 256 B, rows 8..15
+// shifted by 128 B (bank spread), rounded up to a multiple of 128.
+constexpr int kGroupXTileBytes = 16 * 256 + 256;
+
+// Ring slot of kinds 2 and 3: kind 2 per wave 1 KB of weights and 1 KB of scales, plus the x rows
+// of the token group (bm rows x 256 B); kind 3 per n16 block 1 KB of weights and 64 B of scales,
+// plus the x rows with the tile padding above.
 constexpr int prefill_lds_bytes(int cfg) {
-    return kPrefillTable[cfg].kind >= 2
+    return kPrefillTable[cfg].kind == 3
+               ? (kPrefillTable[cfg].depth + 1) *
+                     (1088 * kPrefillTable[cfg].bn / 16 + kPrefillTable[cfg].bm / 16 * kGroupXTileBytes)
+           : kPrefillTable[cfg].kind == 2
                ? (kPrefillTable[cfg].depth + 1) *
                      (2048 * kPrefillTable[cfg].waves_n + kPrefillTable[cfg].bm / 4 * 1024)   // ring slots
                : 2 * kPrefillTable[cfg].bm * kLdsRowBytes;

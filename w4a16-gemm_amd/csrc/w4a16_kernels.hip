@@ -958,19 +958,28 @@ prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     }
 }
 
-// Prefill for token groups (any M): W waves per workgroup, one per n16 block, share the x rows of
-// one group of 16*TM tokens (grid: ceil(M / 16TM) token groups x ceil(N / 16W) column groups).
+// Prefill for token groups (any M): W waves per workgroup, NB n16 blocks per wave, share the x
+// rows of one group of 16*TM tokens (grid: ceil(M / 16TM) token groups x ceil(N / 16 W NB) column
+// groups).
 //
-// prefill_stream_kernel with the x rows shared.  Each wave still walks the whole K range of its
-// n16 block with the refill-ahead ring of D+1 chunk-pair slots, but a slot holds the x rows of the
-// pair once for the W waves: wave w issues x loads [w XD/W, (w+1) XD/W) besides its own weights
-// and scales, waits for its own loads of pair p, and one barrier then publishes all of pair p and
-// retires every wave's reads of pair p-1, whose slot the refill (pair p+D) reuses.  So the x
-// traffic and the LDS of a group are shared W ways, more waves fit per CU, and large M runs as
-// independent token groups (their weights re-read from L2).  Same A and B operands and the same
-// MFMA order per accumulator as every other prefill config, so the output is bit-identical.
-// Waves whose n16 block lies past N work on the last block (clamped) and store nothing.
-template <int TM, int D, int W>
+// prefill_stream_kernel with the x rows shared.  Each wave walks the whole K range of its NB
+// n16 blocks with the refill-ahead ring of D+1 chunk-pair slots, but a slot holds the x rows of
+// the pair once for the W waves: wave w issues x loads [w XD/W, (w+1) XD/W) besides its own
+// weights and scales, waits for its own loads of pair p, and one barrier then publishes all of
+// pair p and retires every wave's reads of pair p-1, whose slot the refill (pair p+D) reuses.  So
+// the x traffic and the LDS of a group are shared W ways, and large M runs as independent token
+// groups (their weights re-read from L2).  Every x operand a wave reads feeds NB MFMAs: the LDS
+// reads per MFMA fall as 1/NB.  Same A and B operands and the same MFMA order per accumulator
+// as every other prefill config, so the output is bit-identical.  Blocks past N are computed on
+// the last block (clamped) and not stored.
+//
+// x layout in a slot: token tile t (16 rows) at t * XT; row r at r * 256, rows 8..15 shifted by
+// 128 bytes; the 16-byte global segment g of a row sits at position g ^ (r % 8).  The B operand
+// of lane (kb, j) -- dwords 16h + 4c + kb (c = 0..3) of row j's chunk cc -- is read as four 4-byte
+// LDS reads, with no cross-lane transpose.  Per wave, a slot holds NB KB of weights and the
+// pair's scales ([block][chunk][16 channels], 64 B per block).  The ring loop is unrolled by its
+// size, so every LDS offset is an instruction immediate.
+template <int TM, int D, int W, int NB>
 __global__ void __launch_bounds__(64 * W)
 prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                      const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
@@ -978,11 +987,15 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     constexpr int S = D + 1;                                 // ring slots
     constexpr int XD = 4 * TM;                               // x loads per pair (4 rows each)
     constexpr int XW = XD / W;                               // x loads per wave and pair
-    constexpr int XOFF = 2048 * W;                           // x region of a slot
-    constexpr int SLOT = XOFF + XD * 1024;                   // W x (weights, scales), 16 TM rows x 256 B
-    constexpr int OPS = 1 + XW + 1;                          // weights, x share, scales
+    constexpr int WR = NB * 1024 + NB * 64;                  // per wave: weights, scales
+    constexpr int XOFF = WR * W;                             // x region of a slot
+    constexpr int XT = kGroupXTileBytes;                     // bytes per 16-row token tile
+    constexpr int SLOT = XOFF + TM * XT;
+    constexpr int OPS = NB + XW + 1;                         // weights, x share, scales
     static_assert(XD % W == 0, "x loads must split evenly over the waves");
+    static_assert(4 * NB <= 64, "scale pieces of one pair must fit one load");
     static_assert((D - 1) * OPS <= 63, "too many loads in flight for vmcnt");
+    static_assert((S - 1) * SLOT + (TM - 1) * XT + 128 < 65536, "x read offsets must fit the LDS offset field");
     __shared__ __attribute__((aligned(16))) char wl[S * SLOT];
 
     const int lane = threadIdx.x & 63;
@@ -993,130 +1006,177 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // column group's weights in that XCD's L2.
     const int G = gridDim.x;
     const int G8 = G >> 3;
-    const int b = blockIdx.x;
-    const int tile = b < (G8 << 3) ? (b & 7) * G8 + (b >> 3) : b;
+    const int bid = blockIdx.x;
+    const int tile = bid < (G8 << 3) ? (bid & 7) * G8 + (bid >> 3) : bid;
     const int tg = tile % groups_m;
     const int ng = tile / groups_m;
     const int NBLK = N >> 4;
-    const int nb_raw = ng * W + wave;
-    const int nb = min(nb_raw, NBLK - 1);
+    const int nb0_raw = (ng * W + wave) * NB;                // first n16 block of the wave
     const int m0 = tg * 16 * TM;
     const int KC = K >> 6;
     const int npair = KC >> 1;
     const uint32_t lds = (uint32_t)reinterpret_cast<uintptr_t>(wl);
 
-    // Weights: lane j fills segment j & 31 of chunk j >> 5 with packed lane 4*(seg % 8) + seg / 8.
+    // Weights of block b: lane j fills segment j & 31 of chunk j >> 5 with packed lane
+    // 4*(seg % 8) + seg / 8.
     const int wseg = lane & 31;
-    const u4* wsrc = Wp + ((size_t)nb * KC + (lane >> 5)) * 32 + 4 * (wseg & 7) + (wseg >> 3);
-    // x: lane j of load q fills row r = (64q + j) / 16 of the group, segment j % 16, with global
-    // segment (j % 16) ^ (r % 8) of row min(m0 + r, M - 1).  This wave issues loads q = wave*XW + i.
+    const u4* wsrc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+        wsrc[b] = Wp + ((size_t)min(nb0_raw + b, NBLK - 1) * KC + (lane >> 5)) * 32 + 4 * (wseg & 7) + (wseg >> 3);
+    // x: load q fills rows r0 = 4 (q % 4) .. r0 + 3 of token tile q / 4; lane j fills row
+    // r0 + j / 16, position j % 16, with global segment (j % 16) ^ (row % 8) of token
+    // min(m0 + 16 (q / 4) + row, M - 1).  This wave issues loads q = wave*XW + i.
     const uint16_t* xsrc[XW];
 #pragma unroll
     for (int i = 0; i < XW; ++i) {
         const int q = wave * XW + i;
-        const int r = (64 * q + lane) >> 4;
-        xsrc[i] = x + (size_t)min(m0 + r, M - 1) * K + (((lane & 15) ^ (r & 7)) * 8);
+        const int r = 4 * (q & 3) + (lane >> 4);
+        xsrc[i] = x + (size_t)min(m0 + 16 * (q >> 2) + r, M - 1) * K + (((lane & 15) ^ (r & 7)) * 8);
     }
-    // Scales: the pair's 2 chunks x 16 channels are 4 16-byte pieces (chunk c = (j >> 1) & 1,
-    // channels 8*(j & 1)..+7); lane j loads piece j & 3, so the other lanes repeat them.
-    const uint16_t* ssrc = scales + (size_t)nb * 16 + (lane & 1) * 8;
-    const int scc = (lane >> 1) & 1;
-    auto issue = [&](int p, int s) {
-        char* sl = wl + s * SLOT;
-        __builtin_amdgcn_global_load_lds((const void*)(wsrc + (size_t)p * 64),
-                                         (__attribute__((address_space(3))) void*)(sl + wave * 2048), 16, 0, 0);
+    // Scales: lane e < 4 NB loads piece e & 3 of block e / 4 (chunk (e >> 1) & 1, channels
+    // 8 (e & 1)..+7), 16 bytes, into byte 16 e of the wave's scale region.
+    const int se = min(lane, 4 * NB - 1);
+    const uint16_t* ssrc = scales + (size_t)min(nb0_raw + (se >> 2), NBLK - 1) * 16 + (se & 1) * 8;
+    const int scc = (se >> 1) & 1;
+    auto issue = [&](int p, auto slot) {
+        char* sl = wl + decltype(slot)::value * SLOT;
 #pragma unroll
-        for (int i = 0; i < XW; ++i)
+        for (int b = 0; b < NB; ++b)
+            __builtin_amdgcn_global_load_lds((const void*)(wsrc[b] + (size_t)p * 64),
+                                             (__attribute__((address_space(3))) void*)(sl + wave * WR + b * 1024), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < XW; ++i) {
+            const int q = wave * XW + i;
+            const int r0 = 4 * (q & 3);
             __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + (size_t)p * 128),
-                                             (__attribute__((address_space(3))) void*)(sl + XOFF + (wave * XW + i) * 1024),
+                                             (__attribute__((address_space(3))) void*)(sl + XOFF + (q >> 2) * XT + r0 * 256 +
+                                                                                       (r0 >= 8 ? 128 : 0)),
                                              16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)((2 * p + scc) >> gshift) * N),
-                                         (__attribute__((address_space(3))) void*)(sl + wave * 2048 + 1024), 16, 0, 0);
+        }
+        if (lane < 4 * NB)
+            __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)((2 * p + scc) >> gshift) * N),
+                                             (__attribute__((address_space(3))) void*)(sl + wave * WR + NB * 1024), 16, 0, 0);
         asm volatile("" ::: "memory");
     };
 
-    uint32_t xoff[TM][2][2];
+    // Per-lane LDS bases (slot 0, token tile 0, chunk 0, block 0): x dword kb of global segment
+    // 4h + c of row li; weights segment (li % 8) + 8 kb; scales of channel li.
+    uint32_t xb[2][4];
 #pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        const int r = 16 * t + li;                           // row within the group (rows past M repeat M-1)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) xoff[t][cc][h] = XOFF + r * 256 + (((cc * 8 + 4 * h + kb) ^ (r & 7)) << 4);
-    }
-    const uint32_t woff = wave * 2048 + (((li & 7) + 8 * kb) << 4);
-    const uint32_t soff = wave * 2048 + 1024 + (li >> 3) * 16 + (li & 7) * 2;     // + 32 * chunk
+        for (int c = 0; c < 4; ++c)
+            xb[h][c] = lds + XOFF + li * 256 + (li >> 3) * 128 + (((4 * h + c) ^ (li & 7)) << 4) + 4 * kb;
+    const uint32_t wb = lds + wave * WR + (((li & 7) + 8 * kb) << 4);
+    const uint32_t sb = lds + wave * WR + NB * 1024 + (li >> 3) * 16 + (li & 7) * 2;   // + 64 block + 32 chunk
     const Dq d = dq_setup(lane);
-    f4 acc[TM];
+    f4 acc[TM][NB];
 #pragma unroll
-    for (int t = 0; t < TM; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
 
-    auto consume = [&](int s) {
-        const uint32_t base = lds + s * SLOT;
-        u4 wv[2], xv[TM][2][2];
-        uint32_t sv[2];
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) wv[cc] = lds_read_u4(base + cc * 512 + woff);
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) sv[cc] = lds_read_u16(base + soff + cc * 32);
-#pragma unroll
-        for (int t = 0; t < TM; ++t)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) xv[t][cc][h] = lds_read_u4(base + xoff[t][cc][h]);
+    auto consume = [&](auto slot) {
+        constexpr int SO = decltype(slot)::value * SLOT;
+        u4 wv[NB][2], xv[TM][2][2];
+        uint32_t sv[NB][2];
+        static_for<0, NB>([&](auto b) {
+            static_for<0, 2>([&](auto cc) {
+                constexpr int B = decltype(b)::value, C = decltype(cc)::value;
+                wv[B][C] = lds_read_u4_at<SO + B * 1024 + C * 512>(wb);
+                sv[B][C] = lds_read_u16_at<SO + B * 64 + C * 32>(sb);
+            });
+        });
+        static_for<0, TM>([&](auto t) {
+            static_for<0, 2>([&](auto cc) {
+                static_for<0, 2>([&](auto h) {
+                    constexpr int O = SO + decltype(t)::value * XT + decltype(cc)::value * 128;
+                    constexpr int H = decltype(h)::value;
+                    xv[decltype(t)::value][decltype(cc)::value][H] =
+                        u4{lds_read_u32_at<O>(xb[H][0]), lds_read_u32_at<O>(xb[H][1]),
+                           lds_read_u32_at<O>(xb[H][2]), lds_read_u32_at<O>(xb[H][3])};
+                });
+            });
+        });
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            bind_after_wait(wv[cc]);
-            bind_after_wait(sv[cc]);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) { bind_after_wait(wv[b][cc]); bind_after_wait(sv[b][cc]); }
 #pragma unroll
             for (int t = 0; t < TM; ++t) { bind_after_wait(xv[t][cc][0]); bind_after_wait(xv[t][cc][1]); }
         }
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            const h2 s2 = scale2((uint16_t)sv[cc]);
-            const h8 a0 = dq_frag(wv[cc].x, wv[cc].y, d, s2);
-            const h8 a1 = dq_frag(wv[cc].z, wv[cc].w, d, s2);
+            h8 a0[NB], a1[NB];
 #pragma unroll
-            for (int t = 0; t < TM; ++t) acc[t] = mfma16x16x32(a0, __builtin_bit_cast(h8, xpose_rows(xv[t][cc][0])), acc[t]);
+            for (int b = 0; b < NB; ++b) {
+                const h2 s2 = scale2((uint16_t)sv[b][cc]);
+                const u4 w = wv[b][cc];
+                a0[b] = dq_frag(w.x, w.y, d, s2);
+                a1[b] = dq_frag(w.z, w.w, d, s2);
+            }
 #pragma unroll
-            for (int t = 0; t < TM; ++t) acc[t] = mfma16x16x32(a1, __builtin_bit_cast(h8, xpose_rows(xv[t][cc][1])), acc[t]);
+            for (int t = 0; t < TM; ++t) {
+                const u4 b0 = xv[t][cc][0];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[t][b] = mfma16x16x32(a0[b], __builtin_bit_cast(h8, b0), acc[t][b]);
+            }
+#pragma unroll
+            for (int t = 0; t < TM; ++t) {
+                const u4 b1 = xv[t][cc][1];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[t][b] = mfma16x16x32(a1[b], __builtin_bit_cast(h8, b1), acc[t][b]);
+            }
         }
     };
 
-    // Prologue: pairs 0..D-1 (npair >= D, checked by the planner).  Steady state: wait for this
-    // wave's loads of pair p, barrier (all of pair p landed; every wave is done with pair p-1),
-    // refill pair p-1's slot with pair p + D, compute pair p.  Drain: the last D pairs.  The
-    // barrier is a bare s_barrier: the explicit vmcnt wait has completed this wave's loads of pair
-    // p (a completed direct-to-LDS load is in LDS) and consume() ends with lgkmcnt(0), which is all
-    // the ordering the ring needs; __syncthreads() would also wait for vmcnt(0), draining the
-    // loads of the next D pairs at every step.
-#pragma unroll
-    for (int s = 0; s < D; ++s) issue(s, s);
-    int sc = 0, si = D;
+    // Prologue: pairs 0..D-1 in slots 0..D-1 (npair >= D, checked by the planner).  Steady state,
+    // S pairs per iteration: wait for this wave's loads of pair p, barrier (all of pair p landed;
+    // every wave is done with pair p-1), refill pair p-1's slot with pair p + D, compute pair p;
+    // pair p lives in slot p % S.  Tail: the remaining (< S) steady steps, then the last D pairs.
+    // The barrier is a bare s_barrier: the explicit vmcnt wait has completed this wave's loads of
+    // pair p (a completed direct-to-LDS load is in LDS) and consume() ends with lgkmcnt(0), which
+    // is all the ordering the ring needs; __syncthreads() would also wait for vmcnt(0), draining
+    // the loads of the next D pairs at every step.
+    static_for<0, D>([&](auto s) { issue(s, s); });
+    const int nsteady = npair - D;
     int p = 0;
-    for (; p + D < npair; ++p) {
-        wait_vmcnt((D - 1) * OPS);
-        __builtin_amdgcn_s_barrier();
-        issue(p + D, si);
-        consume(sc);
-        sc = sc + 1 == S ? 0 : sc + 1;
-        si = si + 1 == S ? 0 : si + 1;
+    for (; p + S <= nsteady; p += S) {
+        static_for<0, S>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            wait_vmcnt((D - 1) * OPS);
+            __builtin_amdgcn_s_barrier();
+            issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
+            consume(t);
+        });
     }
-#pragma unroll
-    for (int t = 0; t < D; ++t) {
-        wait_vmcnt((D - 1 - t) * OPS);
-        __builtin_amdgcn_s_barrier();
-        consume(sc);
-        sc = sc + 1 == S ? 0 : sc + 1;
-    }
+    static_switch<0, S>(nsteady - p, [&](auto r) {
+        constexpr int R = decltype(r)::value;
+        static_for<0, R>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            wait_vmcnt((D - 1) * OPS);
+            __builtin_amdgcn_s_barrier();
+            issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
+            consume(t);
+        });
+        static_for<0, D>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            wait_vmcnt((D - 1 - T) * OPS);
+            __builtin_amdgcn_s_barrier();
+            consume(std::integral_constant<int, (R + T) % S>{});
+        });
+    });
 
-    if (nb_raw < NBLK) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int nb = nb0_raw + b;
+        if (nb >= NBLK) break;
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
             const int m = m0 + 16 * t + li;
-            if (m < M) *reinterpret_cast<u2*>(y + (size_t)m * N + nb * 16 + 4 * kb) = pack_f16x4(acc[t]);
+            if (m < M) *reinterpret_cast<u2*>(y + (size_t)m * N + nb * 16 + 4 * kb) = pack_f16x4(acc[t][b]);
         }
     }
 }
@@ -1145,6 +1205,10 @@ W4A16_PREFILL_CFG(8)
 W4A16_PREFILL_CFG(9)
 W4A16_PREFILL_CFG(10)
 W4A16_PREFILL_CFG(11)
+W4A16_PREFILL_CFG(12)
+W4A16_PREFILL_CFG(13)
+W4A16_PREFILL_CFG(14)
+W4A16_PREFILL_CFG(15)
 #undef W4A16_PREFILL_CFG
 
 template <int CFG>
@@ -1154,8 +1218,8 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
     const int gshift = p.G == 128 ? 1 : 0;
     const int tiles_m = (p.M + C::BM - 1) / C::BM;
     if constexpr (kPrefillTable[CFG].kind == 3)
-        hipLaunchKernelGGL((prefill_group_kernel<C::BM / 16, kPrefillTable[CFG].depth, C::WN>), dim3(p.grid),
-                           dim3(64 * C::WN), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
+        hipLaunchKernelGGL((prefill_group_kernel<C::BM / 16, kPrefillTable[CFG].depth, C::WN, C::BN / (16 * C::WN)>),
+                           dim3(p.grid), dim3(64 * C::WN), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
     else if constexpr (kPrefillTable[CFG].kind == 2)
         hipLaunchKernelGGL((prefill_stream_kernel<C::BM / 16, kPrefillTable[CFG].depth>), dim3(p.grid), dim3(64), 0, st,
                            Wp, x, s, y, p.M, p.N, p.K, gshift);
@@ -1252,6 +1316,10 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
             case 9: e = launch_prefill<9>(p, wp, x, scales, y, st); break;
             case 10: e = launch_prefill<10>(p, wp, x, scales, y, st); break;
             case 11: e = launch_prefill<11>(p, wp, x, scales, y, st); break;
+            case 12: e = launch_prefill<12>(p, wp, x, scales, y, st); break;
+            case 13: e = launch_prefill<13>(p, wp, x, scales, y, st); break;
+            case 14: e = launch_prefill<14>(p, wp, x, scales, y, st); break;
+            case 15: e = launch_prefill<15>(p, wp, x, scales, y, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }

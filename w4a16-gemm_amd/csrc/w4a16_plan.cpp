@@ -85,15 +85,24 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //  * M <= 32 while N/16 blocks are at most 2x the CU count: one wave per n16 block over the
     //    whole K (prefill_stream_kernel; K = 14336, N = 4096: 52 vs 155 us for 16 x 128 tiles and
     //    64 us for token groups; at N = 14336, 896 blocks, token groups win: 21 vs 35 us);
-    //  * token groups of 32 rows, 4 waves sharing x (prefill_group_kernel), while the waves
-    //    (M/32 groups x N/16 blocks) are at most 12 per CU: e.g. K = 14336, N = 4096, M = 128:
-    //    65 vs 152 us; N = 28672, M = 32: 31 vs 49 us;
+    //  * token groups of 32 rows with two n16 blocks per wave (every x operand read feeds two
+    //    MFMAs) while their waves (M/32 groups x N/32 block pairs) number 4..12 per CU, 3 pairs
+    //    in flight up to 8 per CU, else 2: e.g. M = 128, N = 14336: 32.9 vs 45.7 us;
+    //    M = 512, N = 6144: 46.4 vs 53.8 us for 128 x 128 tiles;
+    //  * token groups of 32 rows, one n16 block per wave, while the waves (M/32 groups x N/16
+    //    blocks) are at most 12 per CU: e.g. K = 14336, N = 4096, M = 128: 60 vs 77 us with two
+    //    blocks per wave (too few waves); N = 28672, M = 32: 25.6 vs 49 us;
     //  * token groups of 64 rows while those waves are at most 8 per CU (N = 4096, M = 512: 43 vs
     //    46 us; N = 28672, M = 64: 45 vs 50 us);
     //  * then the wide tiles, which beat the 16..128-row tiles for every larger size measured
     //    (N = 6144, M = 512: 54 vs 73 us).
     const double blocks = std::ceil(N / 16.0);
     if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K) && N / 16 <= 2 * lim.cu_count) return 8;
+    const double waves2 = std::ceil(M / 32.0) * std::ceil(N / 32.0);
+    if (waves2 >= 4.0 * cus && waves2 <= 12.0 * cus) {
+        const int cfg = waves2 <= 8.0 * cus ? 14 : 12;
+        if (prefill_occupancy(cfg, lim) > 0 && prefill_shape_ok(cfg, M, K)) return cfg;
+    }
     if (prefill_occupancy(10, lim) > 0 && prefill_shape_ok(10, M, K) &&
         std::ceil(M / 32.0) * blocks <= 12.0 * cus)
         return 10;

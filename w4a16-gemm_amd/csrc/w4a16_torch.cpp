@@ -156,7 +156,7 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
             d["kernel_name"] = std::string(pk[2]) + std::to_string(t.bm / 16) + "," + std::to_string(t.depth) + ">";
         else if (t.kind == 3)
             d["kernel_name"] = std::string(pk[3]) + std::to_string(t.bm / 16) + "," + std::to_string(t.depth) + "," +
-                               std::to_string(t.waves_n) + ">";
+                               std::to_string(t.waves_n) + "," + std::to_string(t.bn / (16 * t.waves_n)) + ">";
         else
         d["kernel_name"] = std::string(pk[t.kind]) + std::to_string(t.bm) + "," + std::to_string(t.bn) + "," +
                            std::to_string(t.waves_m) + "," + std::to_string(t.waves_n) + ">";
