@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 15
+        assert 1 <= p.kernel <= 17
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -164,16 +164,16 @@ def test_prefill_plan_invariants(lib, M, N):
 
 PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128),
                  8: (32, 16), 9: (64, 16), 10: (32, 64), 11: (64, 64), 12: (32, 128), 13: (64, 128), 14: (32, 128),
-                 15: (32, 256)}
+                 15: (32, 256), 16: (16, 64), 17: (16, 64)}
 
 
 @pytest.mark.parametrize("M,N,K,want", [
     (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
     (2048, 14336, 4096, 7),                                                  # partial last round: 128x128
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
-    (17, 4096, 14336, 8), (32, 6144, 4096, 8), (32, 14336, 4096, 10),       # few token rows, few blocks
-    (33, 4096, 4096, 10), (64, 4096, 4096, 10), (128, 4096, 14336, 10),      # token groups of 32
-    (32, 28672, 4096, 10), (48, 14336, 4096, 10),
+    (17, 4096, 14336, 17), (32, 6144, 4096, 17), (32, 14336, 4096, 17),     # token groups of 16
+    (33, 4096, 4096, 17), (64, 4096, 4096, 17), (128, 4096, 14336, 17), (48, 14336, 4096, 17),
+    (32, 28672, 4096, 10),                                                   # token groups of 32
     (128, 14336, 4096, 14), (512, 4096, 4096, 14), (96, 14336, 4096, 14),    # 2 blocks per wave, 3 pairs
     (512, 6144, 4096, 12), (192, 14336, 4096, 12),                           # 2 blocks per wave, 2 pairs
     (256, 14336, 4096, 7), (128, 28672, 4096, 7),                            # moderate sizes: 128x128 wide
@@ -188,7 +188,7 @@ def test_prefill_wide_selection(lib, M, N, K, want):
     tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
     assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4, 12: 4, 13: 4, 14: 4,
-                            15: 4}[p.kernel]
+                            15: 4, 16: 4, 17: 4}[p.kernel]
 
 
 def test_prefill_override(lib, monkeypatch):

@@ -447,8 +447,25 @@ def test_prefill_wide_configs_bitwise_equal(cfg, M, N, K, G, monkeypatch):
     assert torch.equal(gemm(Wp, x[:M // 2 + 1].contiguous(), scales), y[:M // 2 + 1])
 
 
-# Small-M prefill (M = 17..64, chosen automatically): one wave per n16 block over the whole K
-# (alone, or sharing the x rows of a token group), bit-identical to the reference-API variants.
+# One-wave-per-block prefill (configs 8, 9: forced only since 16-token groups took over small M):
+# bit-identical to the reference-API variants, rows past M not stored.
+@pytest.mark.parametrize("cfg,M,N,K,G", [(8, 17, 4096, 4096, 128), (8, 32, 1040, 2048, 64), (8, 20, 16, 1024, 64),
+                                         (9, 40, 512, 14336, 128), (9, 64, 272, 1024, 64), (9, 33, 256, 1024, 128)])
+def test_prefill_stream_configs_bitwise_equal(cfg, M, N, K, G, monkeypatch):
+    torch = torch_cuda()
+    import w4a16_opt
+    monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+    info = w4a16_opt.plan_info(M, N, K, G)
+    assert info["kernel"] == cfg and "prefill_stream_kernel" in info["kernel_name"], info
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=M + cfg)
+    y = gemm(Wp, x, scales)
+    assert torch.equal(y, gemm(Wp, x, scales, variant=4))
+    assert torch.equal(y, gemm(Wp, x, scales, variant=1))
+    assert_close(y, ref_gemm(x, q, scales, G, key))
+
+
+# Small-M prefill (M = 17..64, chosen automatically): token groups of 16 rows sharing x, one wave
+# per n16 block over the whole K, bit-identical to the reference-API variants.
 @pytest.mark.parametrize("M,N,K,G", [(17, 4096, 4096, 128), (32, 1040, 2048, 64), (33, 256, 1024, 128),
                                      (64, 272, 1024, 64), (20, 16, 1024, 64), (40, 512, 14336, 128)])
 def test_prefill_small_m_bitwise_equal(M, N, K, G):
@@ -468,7 +485,7 @@ def test_prefill_small_m_bitwise_equal(M, N, K, G):
 
 # Token-group prefill (configs 10..15, forced through W4A16_PREFILL): 4 waves, 1..4 n16 blocks each, share the x rows of
 # a group of 32 or 64 tokens; any M, N tails (waves past N compute clamped data and store nothing).
-@pytest.mark.parametrize("cfg", [10, 11, 12, 13, 14, 15])
+@pytest.mark.parametrize("cfg", [10, 11, 12, 13, 14, 15, 16, 17])
 @pytest.mark.parametrize("M,N,K,G", [(17, 4096, 4096, 128), (33, 1040, 2048, 64), (100, 272, 1024, 64),
                                      (300, 4112, 4224, 64), (1000, 512, 2048, 128), (64, 16, 1024, 128),
                                      (129, 6144, 4096, 128)])

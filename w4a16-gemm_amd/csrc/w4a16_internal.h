@@ -16,7 +16,7 @@ namespace w4a16 {
 struct PrefillTile {
     int bm, bn, waves_m, waves_n, kind, depth;
 };
-constexpr PrefillTile kPrefillTable[16] = {
+constexpr PrefillTile kPrefillTable[18] = {
     {0, 0, 0, 0, 0, 0},
     {16, 128, 1, 4, 0, 0},     // 1: small batches: 4 waves across N, wave tile 16 x 32
     {32, 128, 1, 4, 0, 0},     // 2: wave tile 32 x 32
@@ -33,9 +33,11 @@ constexpr PrefillTile kPrefillTable[16] = {
     {64, 128, 1, 4, 3, 2},     // 13: groups of 64 tokens, 2 n16 blocks per wave, 2 pairs (forced only)
     {32, 128, 1, 4, 3, 3},     // 14: groups of 32 tokens, 2 n16 blocks per wave, 3 pairs
     {32, 256, 1, 4, 3, 2},     // 15: groups of 32 tokens, 4 n16 blocks per wave, 2 pairs (forced only)
+    {16, 64, 1, 4, 3, 3},      // 16: groups of 16 tokens, 1 n16 block per wave, 3 pairs
+    {16, 64, 1, 4, 3, 4},      // 17: groups of 16 tokens, 1 n16 block per wave, 4 pairs
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 15;     // all prefill configs
+constexpr int kNumPrefillTable = 17;     // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;

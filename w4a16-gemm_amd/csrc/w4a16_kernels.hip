@@ -1209,6 +1209,8 @@ W4A16_PREFILL_CFG(12)
 W4A16_PREFILL_CFG(13)
 W4A16_PREFILL_CFG(14)
 W4A16_PREFILL_CFG(15)
+W4A16_PREFILL_CFG(16)
+W4A16_PREFILL_CFG(17)
 #undef W4A16_PREFILL_CFG
 
 template <int CFG>
@@ -1320,6 +1322,8 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
             case 13: e = launch_prefill<13>(p, wp, x, scales, y, st); break;
             case 14: e = launch_prefill<14>(p, wp, x, scales, y, st); break;
             case 15: e = launch_prefill<15>(p, wp, x, scales, y, st); break;
+            case 16: e = launch_prefill<16>(p, wp, x, scales, y, st); break;
+            case 17: e = launch_prefill<17>(p, wp, x, scales, y, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }

@@ -82,9 +82,10 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     };
     // Rules measured on MI355X (graph-timed sweep of every config over M = 17..1024 on the
     // Llama-3-8B projection shapes):
-    //  * M <= 32 while N/16 blocks are at most 2x the CU count: one wave per n16 block over the
-    //    whole K (prefill_stream_kernel; K = 14336, N = 4096: 52 vs 155 us for 16 x 128 tiles and
-    //    64 us for token groups; at N = 14336, 896 blocks, token groups win: 21 vs 35 us);
+    //  * token groups of 16 rows, one n16 block per wave, 4 pairs in flight, while their waves
+    //    (M/16 groups x N/16 blocks) are at most 12 per CU: every small-M shape measured, e.g.
+    //    K = 14336, N = 4096, M = 32: 42.8 vs 52.6 us for one wave per block over 32 rows
+    //    (prefill_stream_kernel, now forced-only); M = 128: 50 vs 59 us for groups of 32;
     //  * token groups of 32 rows with two n16 blocks per wave (every x operand read feeds two
     //    MFMAs) while their waves (M/32 groups x N/32 block pairs) number 4..12 per CU, 3 pairs
     //    in flight up to 8 per CU, else 2: e.g. M = 128, N = 14336: 32.9 vs 45.7 us;
@@ -97,7 +98,9 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //  * then the wide tiles, which beat the 16..128-row tiles for every larger size measured
     //    (N = 6144, M = 512: 54 vs 73 us).
     const double blocks = std::ceil(N / 16.0);
-    if (prefill_occupancy(8, lim) > 0 && prefill_shape_ok(8, M, K) && N / 16 <= 2 * lim.cu_count) return 8;
+    if (prefill_occupancy(17, lim) > 0 && prefill_shape_ok(17, M, K) &&
+        std::ceil(M / 16.0) * blocks <= 12.0 * cus)
+        return 17;
     const double waves2 = std::ceil(M / 32.0) * std::ceil(N / 32.0);
     if (waves2 >= 4.0 * cus && waves2 <= 12.0 * cus) {
         const int cfg = waves2 <= 8.0 * cus ? 14 : 12;
