@@ -20,6 +20,9 @@
  *                          (kernel.cu:39-41, 72-115, 177-182)
  *   w4a16_gemm (pybind11, src/vectorized/extension.cpp:5-9) is re-exposed by the torch
  *   extension module ``w4a16_opt`` built on top of this ABI.
+ *   w4a16_gemv             the launch of the baseline extension's w4a16_gemv_cuda
+ *                          (src/baseline/kernel.cu:36-72); its pybind11 entry point
+ *                          (src/baseline/extension.cpp:6-8) is re-exposed by ``w4a16_ext``.
  */
 #ifndef W4A16_H_
 #define W4A16_H_
@@ -109,6 +112,24 @@ int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
  * Returns W4A16_OK, W4A16_ERR_INVALID (message via w4a16_last_error) or W4A16_ERR_HIP. */
 int w4a16_quantize_pack(const void* W, int w_is_fp32, int64_t N, int64_t K, int64_t G,
                         int32_t* Wp, uint16_t* scales, void* stream);
+
+/* Largest K that w4a16_gemv accepts: its per-digit int32 sums are exact up to this size. */
+#define W4A16_GEMV_MAX_K (1 << 20)
+
+/* Baseline W4A16 GEMV of the reference's second extension (src/baseline/kernel.cu:8-72), a
+ * different weight format from w4a16_launch's:
+ *   W  : int32 [N, K/8] row-major; nibble j (bits 4j..4j+3) of word k/8 of row n is the signed
+ *        4-bit weight wv(n, k) (values 8..15 are -8..-1), k = 8*(k/8) + j   (kernel.cu:19-28)
+ *   A  : fp16 bits [K];  sW, zW : fp16 bits [N] per-row scale and zero;  C : fp16 bits [N]
+ *   C[n] = fp16_rn((acc - zW[n]) * sW[n]) in fp32                          (kernel.cu:31-33)
+ * acc is the exact sum of wv(n, k) * A[k] rounded once to fp32 (the reference sums in fp32 in k
+ * order; the two differ by that order's rounding error only).  Inf and NaN inputs give the IEEE
+ * result of the sum.  K % 8 == 0, 0 <= K <= W4A16_GEMV_MAX_K; W 4-byte aligned, the others 2-byte
+ * aligned (16-byte alignment of W with K % 32 == 0, and of A, selects wider loads).  Asynchronous
+ * on `stream`, allocates nothing.  Returns W4A16_OK, W4A16_ERR_INVALID (message via
+ * w4a16_last_error) or W4A16_ERR_HIP. */
+int w4a16_gemv(const int32_t* W, const uint16_t* A, const uint16_t* sW, const uint16_t* zW, uint16_t* C,
+               int64_t N, int64_t K, void* stream);
 
 /* Query the limits of HIP device `device` (cached per device, thread-safe). */
 int w4a16_query_device(int device, w4a16_device_limits* lim);

@@ -33,6 +33,7 @@ def lib():
         L.w4a16_oracle_forward.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_int, P, P, ctypes.c_int]
         L.w4a16_oracle_max_threads.restype = ctypes.c_int
+        L.w4a16_oracle_gemv.argtypes = [P, P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P]
         _lib = L
     return _lib
 
@@ -81,6 +82,25 @@ def forward(Wp: np.ndarray, x: np.ndarray, scales: np.ndarray, N: int, K: int, G
     if rc:
         raise RuntimeError(f"w4a16_oracle_forward failed ({rc})")
     return y32, y16
+
+
+def gemv(W: np.ndarray, A: np.ndarray, sW: np.ndarray, zW: np.ndarray, exact: bool = True) -> np.ndarray:
+    """Baseline GEMV (reference src/baseline/kernel.cu:8-34): fp16 [N].
+
+    W int32 [N, K/8]; A fp16 [K]; sW, zW fp16 [N].  exact=False sums in the reference's fp32 k
+    order; exact=True rounds the exact sum once (the contract of the GPU kernel)."""
+    W = np.ascontiguousarray(W, dtype=np.int32)
+    A = np.ascontiguousarray(A, dtype=np.float16)
+    sW = np.ascontiguousarray(sW, dtype=np.float16)
+    zW = np.ascontiguousarray(zW, dtype=np.float16)
+    N, K = W.shape[0], A.shape[0]
+    if W.shape != (N, K // 8) or sW.shape != (N,) or zW.shape != (N,):
+        raise ValueError("W must be [N, K/8], sW and zW [N]")
+    out = np.empty(N, dtype=np.float16)
+    rc = lib().w4a16_oracle_gemv(_p(W), _p(A), _p(sW), _p(zW), N, K, int(bool(exact)), _p(out))
+    if rc:
+        raise ValueError(f"w4a16_oracle_gemv failed ({rc}): K must be a multiple of 8 (and <= 2^20 when exact)")
+    return out
 
 
 def h2f(bits: int) -> float:

@@ -14,6 +14,8 @@
  *   - the fp32 reference GEMM over dequantised      tests/quant.py:83-85
  *     weights (y = x.float() @ Wdeq.float().T), and the fp16 output rounding of the op
  *     (src/vectorized/prefill.cuh:178-181, __floats2half2_rn)
+ *   - the baseline GEMV of the second extension     src/baseline/kernel.cu:8-34
+ *     (w4a16_ext.w4a16_gemv): in the reference's fp32 k order, and as the exact sum rounded once
  *
  * fp16 <-> fp32 conversions are written here from the IEEE 754 binary16 definition.
  */
@@ -206,4 +208,68 @@ int w4a16_oracle_max_threads(void) {
 #else
     return 1;
 #endif
+}
+
+/*
+ * Baseline GEMV of the reference's second extension, w4a16_ext.w4a16_gemv
+ * (src/baseline/kernel.cu:8-34).  W int32 [N, K/8] row-major; nibble j of word k/8 of row n is
+ * the weight at k = 8*(k/8) + j, read as a signed 4-bit value (kernel.cu:26-27).  A fp16 [K];
+ * sW, zW fp16 [N];  C[n] = fp16_rn((acc - z) * s) with fp32 arithmetic (kernel.cu:31-33).
+ *
+ *   exact = 0: acc in the reference's order, acc += wv * a for k = 0 .. K-1 in fp32
+ *              (kernel.cu:20-30; each product is exact in fp32, so an fma gives the same acc).
+ *   exact = 1: acc = the exact sum rounded once to fp32 (the GPU kernel's contract).  Finite fp16
+ *              values are integers in units of 2^-24 below 2^40 in magnitude, so the sum is an
+ *              exact int64 for K <= 2^20.  Non-finite terms take their IEEE class, which for a
+ *              sum does not depend on the order: NaN, 0 * inf, or +inf with -inf give NaN.
+ */
+static inline int gemv_weight(const int32_t* W, int n, int k, int K) {
+    const uint32_t word = (uint32_t)W[(size_t)n * (size_t)(K / 8) + (size_t)(k / 8)];
+    const int nib = (int)((word >> (4 * (k % 8))) & 15u);
+    return nib >= 8 ? nib - 16 : nib;
+}
+
+int w4a16_oracle_gemv(const int32_t* W, const uint16_t* A, const uint16_t* sW, const uint16_t* zW,
+                      int N, int K, int exact, uint16_t* C) {
+    if (N < 0 || K < 0 || K % 8 != 0 || (exact && K > (1 << 20))) return 1;
+    int64_t* fx = NULL;
+    if (exact && K > 0) {
+        fx = (int64_t*)malloc((size_t)K * sizeof(int64_t));
+        if (!fx) return 2;
+        for (int k = 0; k < K; ++k) {
+            const uint32_t h = A[k], e = (h >> 10) & 31u, m = h & 1023u;
+            const int64_t mag = e == 0 ? (int64_t)m : (int64_t)(1024u | m) << (e - 1);   /* a * 2^24 */
+            fx[k] = e == 31 ? 0 : (h & 0x8000u) ? -mag : mag;
+        }
+    }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int n = 0; n < N; ++n) {
+        float acc = 0.0f;
+        if (!exact) {
+            for (int k = 0; k < K; ++k) acc += (float)gemv_weight(W, n, k, K) * w4a16_oracle_h2f(A[k]);
+        } else {
+            int64_t sum = 0;
+            int pos = 0, neg = 0, nan = 0;
+            for (int k = 0; k < K; ++k) {
+                const int wv = gemv_weight(W, n, k, K);
+                const uint32_t h = A[k];
+                if (((h >> 10) & 31u) == 31u) {
+                    if ((h & 1023u) || wv == 0) nan = 1;
+                    else if ((wv < 0) != ((h & 0x8000u) != 0)) neg = 1;
+                    else pos = 1;
+                }
+                sum += (int64_t)wv * fx[k];
+            }
+            acc = (float)sum * 0x1p-24f;                  /* int64 -> fp32 rounds to nearest even */
+            if (nan || (pos && neg)) acc = NAN;
+            else if (pos) acc = INFINITY;
+            else if (neg) acc = -INFINITY;
+        }
+        const float t = acc - w4a16_oracle_h2f(zW[n]);
+        C[n] = w4a16_oracle_f2h(t * w4a16_oracle_h2f(sW[n]));
+    }
+    free(fx);
+    return 0;
 }

@@ -7,6 +7,8 @@ Outputs (next to this file, git-ignored, shipped to the GPU box with the tree):
   libw4a16_hip.so              hipcc --offload-arch=gfx950: kernels + C ABI (include/w4a16.h)
   w4a16_opt<EXT_SUFFIX>        host-compiler (g++) PyTorch extension linking libw4a16_hip.so
                                through an $ORIGIN rpath; import it as `w4a16_opt`.
+  w4a16_ext<EXT_SUFFIX>        the same for the baseline GEMV module `w4a16_ext`.
+  libw4a16_bwprobe.so          bandwidth probes of measure_bw.py.
 """
 from __future__ import annotations
 
@@ -23,6 +25,7 @@ INCLUDE = os.path.join(ROOT, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 LIB = os.path.join(HERE, "libw4a16_hip.so")
 EXT = os.path.join(HERE, "w4a16_opt" + sysconfig.get_config_var("EXT_SUFFIX"))
+EXT_GEMV = os.path.join(HERE, "w4a16_ext" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 # gfx950 only; packed-fp32 VALU ops disabled for all device code (-packed-fp32-ops).
 HIPCC_FLAGS = [
@@ -50,6 +53,7 @@ SOURCES = [
     ("w4a16_kernels.hip", []),
     ("w4a16_prefill_wide.hip", ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]),
     ("w4a16_quantize.hip", []),
+    ("w4a16_gemv.hip", []),
     ("w4a16_plan.cpp", []),
 ]
 
@@ -87,7 +91,7 @@ def build_probe() -> str:
     return PROBE
 
 
-def build_ext() -> str:
+def build_ext(name: str = "w4a16_opt", source: str = "w4a16_torch.cpp", out: str = EXT) -> str:
     import torch.utils.cpp_extension as ce
     import torch
 
@@ -95,19 +99,19 @@ def build_ext() -> str:
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     incs = [INCLUDE, CSRC, *ce.include_paths(), sysconfig.get_paths()["include"], os.path.join(ROCM, "include")]
     libdirs = [*ce.library_paths(), os.path.join(ROCM, "lib"), HERE]
-    tmp = EXT + ".tmp"
+    tmp = out + ".tmp"
     cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
-           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=w4a16_opt",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-DTORCH_EXTENSION_NAME={name}",
            "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
            "-Wno-deprecated-declarations",
            *[f"-I{p}" for p in incs],
-           os.path.join(CSRC, "w4a16_torch.cpp"),
+           os.path.join(CSRC, source),
            *[f"-L{p}" for p in libdirs],
            "-lw4a16_hip", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
            "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-o", tmp]
     _run(cmd)
-    os.replace(tmp, EXT)
-    return EXT
+    os.replace(tmp, out)
+    return out
 
 
 def main(argv=None) -> int:
@@ -118,6 +122,7 @@ def main(argv=None) -> int:
     if not a.lib:
         build_probe()
         build_ext()
+        build_ext("w4a16_ext", "w4a16_ext_torch.cpp", EXT_GEMV)
     return 0
 
 

@@ -1,0 +1,278 @@
+// Baseline W4A16 GEMV (the reference's second extension, w4a16_ext.w4a16_gemv):
+//
+//   C[n] = fp16_rn((acc[n] - zW[n]) * sW[n]),   acc[n] = sum_k wv(n, k) * A[k]
+//
+// W int32 [N, K/8] row-major; nibble j (bits 4j..4j+3) of word k/8 of row n is the signed 4-bit
+// weight wv(n, k) at k = 8*(k/8) + j (src/baseline/kernel.cu:19-28).  A fp16 [K]; sW, zW fp16 [N];
+// fp32 epilogue (kernel.cu:31-33).
+//
+// Exact accumulation on the int8 matrix cores.  Every finite fp16 value a is an integer multiple
+// of 2^-24 with |a * 2^24| < 2^40, so X = a * 2^24 is an exact integer.  Written in six signed
+// base-256 digits, X = sum_j L_j * 256^j with L_j in [-128, 127] (the bytes of X + 0x808080808080,
+// each minus 128), the dot product becomes six integer dot products
+//     acc * 2^24 = sum_j 256^j * P_j,   P_j = sum_k wv(n, k) * L_j(k),
+// and P_j is exact in int32 for K <= 2^20 (|wv * L| <= 1024).  One v_mfma_i32_16x16x64_i8 takes
+// 16 rows of signed weight bytes (A operand) against a B operand whose columns 0..5 are the digit
+// planes L_0..L_5 (columns 6..15 zero).  The int64 sum is rounded once to fp32, so the result is
+// the exact dot product correctly rounded, whatever the split of K.  The reference accumulates in
+// fp32 in k order (kernel.cu:22-30); its result differs from this one by that order's rounding
+// error only.  Non-finite inputs follow IEEE semantics, which for this sum do not depend on the
+// order: a NaN term, 0 * inf, or +inf together with -inf give NaN, otherwise any infinite term
+// gives that infinity.
+//
+// Workgroup = 4 waves on 16 rows.  K is processed in segments of 4096: all 256 threads convert
+// the segment's A values into the digit table in LDS (laid out as the B operands), then each wave
+// multiplies a contiguous quarter of the segment's 128-wide superchunks.  Lane (r, g) = (lane %
+// 16, lane / 16) loads 16 bytes of row r per superchunk: the 32 weights at k = 128p + 32g .. +31,
+// two MFMAs' worth (k offsets 0..15 and 16..31 of its group).  The MFMA output tiles of the 4
+// waves (row 4g + i, digit r in lane (r, g), element i) are summed in LDS (exact integers).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "w4a16.h"
+#include "w4a16_device.h"
+#include "w4a16_internal.h"
+
+namespace w4a16 {
+
+namespace {
+
+typedef int32_t i4v __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 16;                  // rows per workgroup (one MFMA row tile)
+constexpr int kWaves = 4;                  // waves per workgroup, splitting each segment's k range
+constexpr int kSeg = 4096;                 // k per digit-table segment
+constexpr int kSuper = 128;                // k per superchunk (16 bytes of a row per lane)
+constexpr int kDigits = 6;                 // base-256 digits of a * 2^24
+constexpr int kSuperBytes = 2 * 4 * kDigits * 16;   // table bytes per superchunk (768)
+constexpr int kMaxSuperPerWave = kSeg / kSuper / kWaves;   // 8
+constexpr uint64_t kDigitBias = 0x808080808080ull;  // 128 * sum_j 256^j
+
+static_assert(kSeg % (kSuper * kWaves) == 0, "segment must split evenly over the waves");
+static_assert(kSeg / 8 == 2 * 256, "the table build gives each thread two 8-k units");
+
+// a * 2^24 + kDigitBias for a finite fp16 a (non-finite values give kDigitBias, i.e. X = 0).
+__device__ __forceinline__ uint64_t biased_fixed(uint32_t h) {
+    const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
+    const uint64_t mag = e == 0 ? (uint64_t)m : (uint64_t)(1024u | m) << (e - 1);
+    const uint64_t v = (h & 0x8000u) ? kDigitBias - mag : kDigitBias + mag;
+    return e == 31 ? kDigitBias : v;
+}
+
+// Digit j (as a signed byte in two's complement) of four biased values, packed little-endian.
+__device__ __forceinline__ uint32_t digit_dword(const uint64_t (&v)[8], int first, int j) {
+    uint32_t d = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d |= (uint32_t)((v[first + 2 * i] >> (8 * j)) & 0xFFu) << (8 * i);
+    return d ^ 0x80808080u;
+}
+
+// Signed bytes of the even (shift 0) or odd (shift 4) nibbles of a word: nibble n becomes
+// n - 16 * (n >= 8).  With u = n ^ 8 (in 0..15), (u + 0x78) ^ 0x80 is that value as a byte and
+// no byte carries into the next.
+__device__ __forceinline__ uint32_t signed_nibbles(uint32_t w, int shift) {
+    const uint32_t u = ((w ^ 0x88888888u) >> shift) & 0x0F0F0F0Fu;
+    return (u + 0x78787878u) ^ 0x80808080u;
+}
+
+// IEEE class of the non-finite terms of row n (only called when A holds inf or NaN).
+// Returns 0 (none), 1 (+inf), 2 (-inf) or 3 (NaN).
+__device__ int nonfinite_class(const uint32_t* __restrict__ wrow, const uint16_t* __restrict__ A, int K) {
+    bool pos = false, neg = false, nan = false;
+    for (int k = 0; k < K; ++k) {
+        const uint32_t h = A[k];
+        if (((h >> 10) & 31u) != 31u) continue;
+        const int nib = (int)((wrow[k >> 3] >> (4 * (k & 7))) & 15u);
+        const int wv = nib >= 8 ? nib - 16 : nib;
+        if ((h & 1023u) != 0 || wv == 0) nan = true;
+        else if ((wv < 0) != ((h & 0x8000u) != 0)) neg = true;
+        else pos = true;
+    }
+    return nan || (pos && neg) ? 3 : pos ? 1 : neg ? 2 : 0;
+}
+
+// WVEC: rows are 16-byte aligned (W 16-byte aligned and K % 32 == 0), one 16-byte load per lane
+// and superchunk; otherwise four 4-byte loads.  Loads past the row's end are redirected to its
+// first word: their digits are zero (the table is zero for k >= K), so they add nothing.
+// XVEC: A is 16-byte aligned (one 16-byte load per 8 values); otherwise eight 2-byte loads.
+template <bool WVEC, bool XVEC>
+__global__ void __launch_bounds__(256)
+gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, const uint16_t* __restrict__ sW,
+            const uint16_t* __restrict__ zW, uint16_t* __restrict__ C, int N, int K) {
+    __shared__ __align__(16) uint8_t table[kSeg / kSuper * kSuperBytes];
+    __shared__ int32_t part[kWaves][kRows][8];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int row0 = blockIdx.x * kRows;
+    const int kw = K >> 3;                                   // words per row
+    const uint32_t* __restrict__ wrow = W + (size_t)min(row0 + r, N - 1) * kw;
+    i4v acc = {0, 0, 0, 0};
+    int nonfinite = 0;
+
+    for (int seg = 0; seg < K; seg += kSeg) {
+        const int seglen = min(kSeg, K - seg);
+        const int nsc = (seglen + kSuper - 1) / kSuper;      // superchunks in this segment
+        const int per = (nsc + kWaves - 1) / kWaves;         // superchunks per wave (<= 8)
+        const int p0 = wave * per;
+
+        // A values of this thread's two 8-k units (loaded first: their wait leaves the weight
+        // loads below in flight).
+        u4 xa[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int k0 = seg + 8 * (tid + 256 * t);
+            const uint16_t* src = A + (k0 < K ? k0 : 0);
+            if constexpr (XVEC) {
+                xa[t] = *reinterpret_cast<const u4*>(src);
+            } else {
+                uint32_t d[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
+                xa[t] = u4{d[0], d[1], d[2], d[3]};
+            }
+        }
+        // This wave's weights: superchunks p0 .. p0 + per - 1.
+        u4 wq[kMaxSuperPerWave];
+#pragma unroll
+        for (int i = 0; i < kMaxSuperPerWave; ++i) {
+            if (i >= per) break;
+            const int wi = ((seg + (p0 + i) * kSuper) >> 3) + 4 * g;   // first word of the lane's 32 weights
+            if constexpr (WVEC) {
+                wq[i] = *reinterpret_cast<const u4*>(wrow + (wi + 4 <= kw ? wi : 0));
+            } else {
+                uint32_t d[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d[e] = wrow[wi + e < kw ? wi + e : 0];
+                wq[i] = u4{d[0], d[1], d[2], d[3]};
+            }
+        }
+
+        __syncthreads();                                     // previous segment's table reads done
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int u = tid + 256 * t;                     // unit: 8 consecutive k of the segment
+            if (u >= nsc * (kSuper / 8)) continue;
+            const bool in = seg + 8 * u < K;
+            const uint32_t hw[4] = {xa[t].x, xa[t].y, xa[t].z, xa[t].w};
+            uint64_t v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t h = (hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+                nonfinite |= in && ((h >> 10) & 31u) == 31u;
+                v[i] = in ? biased_fixed(h) : kDigitBias;
+            }
+            const int p = u >> 4, rr = (u & 15) * 8;         // superchunk, k offset in it
+            const int gg = rr >> 5, m = (rr >> 4) & 1, h = (rr >> 3) & 1;
+            uint8_t* dst = table + p * kSuperBytes + ((m * 4 + gg) * kDigits) * 16 + 8 * h;
+#pragma unroll
+            for (int j = 0; j < kDigits; ++j) {
+                uint2 pair;
+                pair.x = digit_dword(v, 0, j);               // k offsets 0, 2, 4, 6
+                pair.y = digit_dword(v, 1, j);               // k offsets 1, 3, 5, 7
+                *reinterpret_cast<uint2*>(dst + 16 * j) = pair;
+            }
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int i = 0; i < kMaxSuperPerWave; ++i) {
+            const int p = p0 + i;
+            if (i >= per || p >= nsc) break;
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const uint32_t w0 = m ? wq[i].z : wq[i].x, w1 = m ? wq[i].w : wq[i].y;
+                const i4v a = {(int32_t)signed_nibbles(w0, 0), (int32_t)signed_nibbles(w0, 4),
+                               (int32_t)signed_nibbles(w1, 0), (int32_t)signed_nibbles(w1, 4)};
+                i4v b = {0, 0, 0, 0};
+                if (r < kDigits) {
+                    const u4 t = *reinterpret_cast<const u4*>(table + p * kSuperBytes + ((m * 4 + g) * kDigits + r) * 16);
+                    b = i4v{(int32_t)t.x, (int32_t)t.y, (int32_t)t.z, (int32_t)t.w};
+                }
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+            }
+        }
+    }
+
+    if (r < kDigits) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave][4 * g + i][r] = acc[i];
+    }
+    const bool any_nonfinite = __syncthreads_or(nonfinite);
+    if (tid < kRows && row0 + tid < N) {
+        const int n = row0 + tid;
+        int64_t total = 0;
+#pragma unroll
+        for (int j = 0; j < kDigits; ++j) {
+            int32_t pj = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) pj += part[w][tid][j];
+            total += (int64_t)pj << (8 * j);
+        }
+        float s = (float)total * 0x1p-24f;                   // the exact sum, rounded once
+        if (any_nonfinite) {
+            const int cls = nonfinite_class(W + (size_t)n * kw, A, K);
+            if (cls == 3) s = __builtin_nanf("");
+            else if (cls == 1) s = __builtin_inff();
+            else if (cls == 2) s = -__builtin_inff();
+        }
+        // fp32 subtract and multiply, then fp16 rounding: two roundings, as the reference's
+        // __float2half((acc - z) * s).  Left alone, the compiler folds the multiply and the
+        // conversion into one v_fma_mixlo_f16, which rounds the exact product once (measured: one
+        // fp16 ulp apart in 1 of 14336 outputs); the empty asm makes the fp32 product a value of
+        // its own.
+        const float z = (float)__builtin_bit_cast(_Float16, zW[n]);
+        const float sc = (float)__builtin_bit_cast(_Float16, sW[n]);
+        float prod = (s - z) * sc;
+        asm volatile("" : "+v"(prod));
+        C[n] = __builtin_bit_cast(uint16_t, (_Float16)prod);
+    }
+}
+
+}  // namespace
+
+}  // namespace w4a16
+
+using namespace w4a16;
+
+extern "C" int w4a16_gemv(const int32_t* W, const uint16_t* A, const uint16_t* sW, const uint16_t* zW,
+                          uint16_t* C, int64_t N, int64_t K, void* stream) {
+    if (N < 0 || K < 0 || N >= (int64_t)1 << 31) {
+        w4a16_set_last_error("dimensions out of range");
+        return W4A16_ERR_INVALID;
+    }
+    if (K % 8 != 0) {
+        w4a16_set_last_error("K must be a multiple of 8");
+        return W4A16_ERR_INVALID;
+    }
+    if (K > W4A16_GEMV_MAX_K) {
+        w4a16_set_last_error("K must be at most 1048576 (exact int32 digit sums)");
+        return W4A16_ERR_INVALID;
+    }
+    if (N == 0) return W4A16_OK;
+    if (!sW || !zW || !C || (K > 0 && (!W || !A))) {             // W and A may be empty when K == 0
+        w4a16_set_last_error("null pointer");
+        return W4A16_ERR_INVALID;
+    }
+    if (reinterpret_cast<uintptr_t>(W) % 4 != 0 ||
+        (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(sW) | reinterpret_cast<uintptr_t>(zW) |
+         reinterpret_cast<uintptr_t>(C)) % 2 != 0) {
+        w4a16_set_last_error("W must be 4-byte aligned, A, sW, zW and C 2-byte aligned");
+        return W4A16_ERR_INVALID;
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)((N + kRows - 1) / kRows));
+    const bool wvec = reinterpret_cast<uintptr_t>(W) % 16 == 0 && K % 32 == 0;
+    const bool xvec = reinterpret_cast<uintptr_t>(A) % 16 == 0;
+    auto kernel = wvec ? (xvec ? gemv_kernel<true, true> : gemv_kernel<true, false>)
+                       : (xvec ? gemv_kernel<false, true> : gemv_kernel<false, false>);
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, reinterpret_cast<const uint32_t*>(W), A, sW, zW, C, (int)N,
+                       (int)K);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        w4a16_set_last_error(hipGetErrorString(e));
+        return W4A16_ERR_HIP;
+    }
+    return W4A16_OK;
+}
