@@ -15,6 +15,10 @@ graphs, benchmarks/bench_gemm.py:36-56) and timed with HIP events on the launch 
 Second leg: prefill TFLOP/s at M=2048, K=8192, N=28672, G=128.
 Third leg: prefill at moderate batch, M=128, K=4096, N=14336, G=64,
 reported against both rooflines (its arithmetic intensity sits just above the ridge point).
+Fourth leg: the baseline GEMV of the reference's second extension (w4a16_ext.w4a16_gemv, its own
+row-major [N, K/8] format) on the configs[0] shape K = N = 4096 and the gate/up shape K = 4096,
+N = 14336; bytes = N*K/2 + 2*K + 6*N per call (W, A, sW, zW, C).  `--workload gemv` prints it
+as the JSON line.
 
 Algorithmic work (the roofline numerator): bytes = N*K/2 + (K/G)*N*2 + M*K*2 + M*N*2 per call,
 flops = 2*M*N*K per call.  Peaks: HBM 8000 GB/s, fp16 dense MFMA 2500 TFLOP/s (MI355X spec).
@@ -46,6 +50,7 @@ DECODE_CASES = [("gate_up", 14336, 4096, m) for m in (1, 4, 8, 16)] + \
 PREFILL_CASE = ("mlp70b", 28672, 8192, 2048)
 MODERATE_CASE = ("gate_up", 14336, 4096, 128, 64)          # M=128, G=64
 GRAPH_STEPS = 12                                             # decode steps captured per graph
+GEMV_CASES = [("decode_c1", 4096, 4096), ("gate_up", 14336, 4096)]   # (name, N, K) of w4a16_ext.w4a16_gemv
 G = 128
 
 
@@ -199,6 +204,63 @@ def bench_moderate(torch, gemm, steps, warmup):
             "kernel": w4a16_opt.plan_info(M, N, K, Gm)["kernel_name"]}
 
 
+def gemv_bytes(N, K):
+    """Algorithmic bytes of one baseline GEMV call: W int4, A, and sW, zW, C fp16."""
+    return N * K // 2 + 2 * K + 6 * N
+
+
+def bench_gemv(torch, steps, warmup):
+    """Baseline GEMV (w4a16_ext.w4a16_gemv) on GEMV_CASES.  One step = one call per case; weights
+    rotate through copies whose working set exceeds twice the Infinity Cache, in HIP graphs."""
+    import w4a16_ext
+    cases, graphs, per_graph = [], [], []
+    for name, N, K in GEMV_CASES:
+        copies = max(2, -(-2 * MALL_BYTES // (N * K // 2)))
+        Ws = [torch.randint(-2**31, 2**31 - 1, (N, K // 8), dtype=torch.int32, device="cuda") for _ in range(copies)]
+        A = torch.randn(K, device="cuda").half()
+        sW = (torch.rand(N, device="cuda") * 0.018 + 0.002).half()
+        zW = torch.randn(N, device="cuda").half()
+        g = graph_of(torch, [lambda W=W: w4a16_ext.w4a16_gemv(W, A, sW, zW) for W in Ws])
+        ms = time_graph(torch, [g], steps, warmup)
+        us = ms * 1e3 / (steps * copies)
+        gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
+        log(f"gemv {name} N={N} K={K}: {us:.2f} us  {gbs:.0f} GB/s")
+        cases.append({"layer": name, "N": N, "K": K, "us": round(us, 3), "GBps": round(gbs, 1),
+                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": copies})
+        del Ws, g
+    total_b = sum(gemv_bytes(c["N"], c["K"]) for c in cases)
+    total_us = sum(c["us"] for c in cases)
+    return {"value": total_b / (total_us * 1e-6) / 1e9, "us_per_step": total_us, "bytes_per_step": total_b,
+            "bytes_per_launch": total_b / len(cases), "avg_launch_us": total_us / len(cases), "cases": cases}
+
+
+def cpu_baseline_gemv(max_seconds=12.0):
+    """The oracle's reference-order loop (fp32 sum in k order, src/baseline/kernel.cu:22-33),
+    repeated on a 256-row slice of the first GEMV case until max_seconds (the rate does not
+    depend on the number of rows)."""
+    import numpy as np
+    from oracle import c_oracle
+    nthreads = c_oracle.max_threads()
+    rng = np.random.default_rng(13)
+    total_b, total_t, rows = 0, 0.0, 0
+    name, N, K = GEMV_CASES[0]
+    R = 256
+    W = rng.integers(-2**31, 2**31, (R, K // 8), dtype=np.int64).astype(np.int32)
+    A = rng.standard_normal(K).astype(np.float16)
+    s = rng.uniform(0.002, 0.02, R).astype(np.float16)
+    z = rng.standard_normal(R).astype(np.float16)
+    c_oracle.gemv(W, A, s, z, exact=False)                 # warm-up
+    while total_t < max_seconds:
+        t0 = time.perf_counter()
+        c_oracle.gemv(W, A, s, z, exact=False)
+        total_t += time.perf_counter() - t0
+        total_b += gemv_bytes(R, K)
+        rows += R
+    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "sample": f"oracle C reference-order GEMV, {rows // R} calls on a {R}-row slice of the {name} shape "
+                      f"(K={K}; {total_t:.2f} s, {nthreads} OpenMP threads, host {os.cpu_count()} cpus)"}
+
+
 def bench_copy(torch, steps):
     """Calibration workload for HBM-traffic counters: an elementwise copy (torch.mul by 1) of a
     64 MiB fp16 tensor reads and writes exactly 64 MiB per launch."""
@@ -318,9 +380,10 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--workload", choices=("decode", "prefill", "quantize", "copy"), default="decode",
-                    help="quantize: device quantise+pack of the prefill weight; "
-                         "copy: HBM-counter calibration kernel (64 MiB elementwise copy), no benchmark line")
+    ap.add_argument("--workload", choices=("decode", "prefill", "quantize", "gemv", "copy"), default="decode",
+                    help="quantize: device quantise+pack of the prefill weight; gemv: the baseline GEMV "
+                         "(w4a16_ext); copy: HBM-counter calibration kernel (64 MiB elementwise copy), no "
+                         "benchmark line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--json", default=None, help="also write the JSON line to this file")
@@ -361,12 +424,36 @@ def main(argv=None) -> int:
             with open(a.json, "w") as f:
                 f.write(line + "\n")
         return 0
+    if a.workload == "gemv":
+        gv = bench_gemv(torch, a.steps, a.warmup)
+        out = {"metric": "baseline GEMV GB/s & %HBM peak (w4a16_ext.w4a16_gemv)",
+               "value": round(gv["value"], 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+               "ms_per_step": round(gv["us_per_step"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+               "vs_baseline": None, "dtype": "int8 MFMA (exact), fp32 epilogue", "data": "synthetic",
+               "config": {"workload": "baseline GEMV, W int32 [N, K/8]; one step = one call each of " +
+                                      ", ".join(f"{n} N={N} K={K}" for n, N, K in GEMV_CASES),
+                          "timing": "HIP graph replay over rotating weight copies, HIP events"},
+               "roofline": {"bound": "hbm", "achieved": round(gv["value"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(gv["value"] / HBM_PEAK_GBS, 4), "traffic": load_traffic("gemv"),
+                            "kernel": "w4a16::gemv_kernel<true, true>",
+                            "bytes_per_launch": gv["bytes_per_launch"],
+                            "avg_launch_us": round(gv["avg_launch_us"], 3)},
+               "cases": gv["cases"]}
+        if not a.no_cpu:
+            out["cpu_baseline"] = cpu_baseline_gemv()
+        line = json.dumps(out)
+        print(line, flush=True)
+        if a.json:
+            with open(a.json, "w") as f:
+                f.write(line + "\n")
+        return 0
     pre = None
     dec = bench_decode(torch, gemm, a.steps, a.warmup) if a.workload == "decode" else None
     if a.workload == "prefill" or not a.no_prefill:
         pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
                             a.warmup if a.workload == "prefill" else 3)
     mod = bench_moderate(torch, gemm, 30, 3) if (dec is not None and not a.no_prefill) else None
+    gv = bench_gemv(torch, 20, 3) if (dec is not None and not a.no_prefill) else None
 
     out = {"metric": "decode GB/s & %HBM peak (M=1..16); prefill TFLOP/s & %MFMA peak (M=2048)"}
     if dec is not None:
@@ -415,9 +502,16 @@ def main(argv=None) -> int:
                          "frac_mfma": round(mod["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
                          "frac_hbm": round(mod["GBs"] / HBM_PEAK_GBS, 4),
                          "flops_per_launch": alg_flops(M, N, K), "bytes_per_launch": alg_bytes(M, N, K, Gm)}}
+    if gv is not None:
+        out["baseline_gemv"] = {"value": round(gv["value"], 1), "unit": "GB/s",
+                                "frac_hbm": round(gv["value"] / HBM_PEAK_GBS, 4),
+                                "us_per_step": round(gv["us_per_step"], 2), "cases": gv["cases"],
+                                "kernel": "w4a16::gemv_kernel<true, true>"}
     if not a.no_cpu:
         if dec is not None:
             out["cpu_baseline"] = cpu_baseline(DECODE_CASES)
+            if gv is not None:
+                out["baseline_gemv"]["cpu_baseline"] = cpu_baseline_gemv(5.0)
             if pre is not None:
                 out["prefill"]["cpu_baseline"] = cpu_baseline_prefill()
         else:

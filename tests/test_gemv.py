@@ -181,7 +181,8 @@ def test_oracle_nonfinite_classes_agree_with_reference_order():
 
 # ----------------------------------------------------------------------------- kernel emulation (CPU)
 
-SEG, SUPER, WAVES, DIGITS = 4096, 128, 4, 6
+SEG, SUPER, WAVES, DIGITS = 4096, 128, 8, 6
+THREADS, PER_WAVE = 64 * WAVES, SEG // SUPER // WAVES
 BIAS = 0x808080808080
 
 
@@ -239,9 +240,8 @@ def emulate_gemv_kernel(W, A, N, K, wvec):
             nsc = (seglen + SUPER - 1) // SUPER
             per = (nsc + WAVES - 1) // WAVES
             table = np.full(SEG // SUPER * 768, 0xEE, dtype=np.uint8)   # poison: unwritten bytes
-            for tid in range(256):
-                for t in range(2):
-                    u = tid + 256 * t
+            for tid in range(THREADS):
+                for u in (tid,):
                     k0 = seg + 8 * u
                     src = k0 if k0 < K else 0
                     assert 0 <= src and (K == 0 or src + 8 <= K)
@@ -258,20 +258,20 @@ def emulate_gemv_kernel(W, A, N, K, wvec):
                                 byte = ((int(v[par + 2 * i]) >> (8 * j)) & 0xFF) ^ 0x80
                                 table[base + 16 * j + 4 * par + i] = byte
             for wave in range(WAVES):
-                p0 = wave * per
-                for i in range(min(per, 8)):
-                    p = p0 + i
+                for i in range(PER_WAVE):
+                    p = wave * per + i
+                    p_load = wave * per + min(i, per - 1)          # loads past the share repeat
                     lanes_words = {}
                     for g in range(4):
                         for r in range(16):
-                            wi = ((seg + p * SUPER) >> 3) + 4 * g
+                            wi = ((seg + p_load * SUPER) >> 3) + 4 * g
                             if wvec:
                                 idx = [wi + e for e in range(4)] if wi + 4 <= kw else [e for e in range(4)]
                             else:
                                 idx = [wi + e if wi + e < kw else 0 for e in range(4)]
                             assert all(0 <= x < kw for x in idx), (seg, p, g, idx)
                             lanes_words[(r, g)] = [int(Wu[rows[r], x]) for x in idx]
-                    if p >= nsc:
+                    if i >= per or p >= nsc:
                         break
                     for m in range(2):
                         Abytes = np.zeros((16, 4, 16), dtype=np.int64)       # [row r, group g, byte]

@@ -20,11 +20,11 @@
 // order: a NaN term, 0 * inf, or +inf together with -inf give NaN, otherwise any infinite term
 // gives that infinity.
 //
-// Workgroup = 4 waves on 16 rows.  K is processed in segments of 4096: all 256 threads convert
-// the segment's A values into the digit table in LDS (laid out as the B operands), then each wave
-// multiplies a contiguous quarter of the segment's 128-wide superchunks.  Lane (r, g) = (lane %
+// Workgroup = 8 waves on 16 rows.  K is processed in segments of 4096: each of the 512 threads
+// converts 8 A values into the digit table in LDS (laid out as the B operands), then each wave
+// multiplies a contiguous eighth of the segment's 128-wide superchunks.  Lane (r, g) = (lane %
 // 16, lane / 16) loads 16 bytes of row r per superchunk: the 32 weights at k = 128p + 32g .. +31,
-// two MFMAs' worth (k offsets 0..15 and 16..31 of its group).  The MFMA output tiles of the 4
+// two MFMAs' worth (k offsets 0..15 and 16..31 of its group).  The MFMA output tiles of the 8
 // waves (row 4g + i, digit r in lane (r, g), element i) are summed in LDS (exact integers).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -40,16 +40,17 @@ namespace {
 typedef int32_t i4v __attribute__((ext_vector_type(4)));
 
 constexpr int kRows = 16;                  // rows per workgroup (one MFMA row tile)
-constexpr int kWaves = 4;                  // waves per workgroup, splitting each segment's k range
+constexpr int kWaves = 8;                  // waves per workgroup, splitting each segment's k range
+constexpr int kThreads = kWaves * 64;
 constexpr int kSeg = 4096;                 // k per digit-table segment
 constexpr int kSuper = 128;                // k per superchunk (16 bytes of a row per lane)
 constexpr int kDigits = 6;                 // base-256 digits of a * 2^24
 constexpr int kSuperBytes = 2 * 4 * kDigits * 16;   // table bytes per superchunk (768)
-constexpr int kMaxSuperPerWave = kSeg / kSuper / kWaves;   // 8
+constexpr int kPerWave = kSeg / kSuper / kWaves;   // superchunks per wave and segment (4)
 constexpr uint64_t kDigitBias = 0x808080808080ull;  // 128 * sum_j 256^j
 
 static_assert(kSeg % (kSuper * kWaves) == 0, "segment must split evenly over the waves");
-static_assert(kSeg / 8 == 2 * 256, "the table build gives each thread two 8-k units");
+static_assert(kSeg / 8 == kThreads, "the table build gives each thread one 8-k unit");
 
 // a * 2^24 + kDigitBias for a finite fp16 a (non-finite values give kDigitBias, i.e. X = 0).
 __device__ __forceinline__ uint64_t biased_fixed(uint32_t h) {
@@ -95,8 +96,12 @@ __device__ int nonfinite_class(const uint32_t* __restrict__ wrow, const uint16_t
 // and superchunk; otherwise four 4-byte loads.  Loads past the row's end are redirected to its
 // first word: their digits are zero (the table is zero for k >= K), so they add nothing.
 // XVEC: A is 16-byte aligned (one 16-byte load per 8 values); otherwise eight 2-byte loads.
+//
+// Segments are double-buffered: the A values and weights of segment s + 1 are requested before
+// the MFMAs of segment s, so their latency overlaps that work.  Every load is issued
+// unconditionally (clamped addresses) so the compiler's waits count exactly the loads in flight.
 template <bool WVEC, bool XVEC>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kThreads)
 gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, const uint16_t* __restrict__ sW,
             const uint16_t* __restrict__ zW, uint16_t* __restrict__ C, int N, int K) {
     __shared__ __align__(16) uint8_t table[kSeg / kSuper * kSuperBytes];
@@ -111,34 +116,29 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
     i4v acc = {0, 0, 0, 0};
     int nonfinite = 0;
 
-    for (int seg = 0; seg < K; seg += kSeg) {
-        const int seglen = min(kSeg, K - seg);
-        const int nsc = (seglen + kSuper - 1) / kSuper;      // superchunks in this segment
-        const int per = (nsc + kWaves - 1) / kWaves;         // superchunks per wave (<= 8)
-        const int p0 = wave * per;
-
-        // A values of this thread's two 8-k units (loaded first: their wait leaves the weight
-        // loads below in flight).
-        u4 xa[2];
+    // superchunks of segment `seg`, and this wave's share (a contiguous range starting at p0)
+    auto shape = [&](int seg, int& nsc, int& per) {
+        nsc = (min(kSeg, K - seg) + kSuper - 1) / kSuper;
+        per = (nsc + kWaves - 1) / kWaves;
+    };
+    // Request the A values of this thread's 8-k unit and this wave's weights for segment `seg`.
+    auto issue = [&](int seg, u4& xa, u4 (&wq)[kPerWave]) {
+        int nsc, per;
+        shape(seg, nsc, per);
+        const int k0 = seg + 8 * tid;
+        const uint16_t* src = A + (k0 < K ? k0 : 0);
+        if constexpr (XVEC) {
+            xa = *reinterpret_cast<const u4*>(src);
+        } else {
+            uint32_t d[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int k0 = seg + 8 * (tid + 256 * t);
-            const uint16_t* src = A + (k0 < K ? k0 : 0);
-            if constexpr (XVEC) {
-                xa[t] = *reinterpret_cast<const u4*>(src);
-            } else {
-                uint32_t d[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) d[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
-                xa[t] = u4{d[0], d[1], d[2], d[3]};
-            }
+            for (int e = 0; e < 4; ++e) d[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
+            xa = u4{d[0], d[1], d[2], d[3]};
         }
-        // This wave's weights: superchunks p0 .. p0 + per - 1.
-        u4 wq[kMaxSuperPerWave];
 #pragma unroll
-        for (int i = 0; i < kMaxSuperPerWave; ++i) {
-            if (i >= per) break;
-            const int wi = ((seg + (p0 + i) * kSuper) >> 3) + 4 * g;   // first word of the lane's 32 weights
+        for (int i = 0; i < kPerWave; ++i) {
+            const int p = wave * per + min(i, per - 1);      // past the share: repeat its last one
+            const int wi = ((seg + p * kSuper) >> 3) + 4 * g;   // first word of the lane's 32 weights
             if constexpr (WVEC) {
                 wq[i] = *reinterpret_cast<const u4*>(wrow + (wi + 4 <= kw ? wi : 0));
             } else {
@@ -148,37 +148,40 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
                 wq[i] = u4{d[0], d[1], d[2], d[3]};
             }
         }
-
-        __syncthreads();                                     // previous segment's table reads done
+    };
+    // Digits of this thread's unit into the table (units past the segment's superchunks are
+    // never read; units past K write zero digits).
+    auto build = [&](int seg, const u4& xa) {
+        int nsc, per;
+        shape(seg, nsc, per);
+        const int u = tid;
+        if (u >= nsc * (kSuper / 8)) return;
+        const bool in = seg + 8 * u < K;
+        const uint32_t hw[4] = {xa.x, xa.y, xa.z, xa.w};
+        uint64_t v[8];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int u = tid + 256 * t;                     // unit: 8 consecutive k of the segment
-            if (u >= nsc * (kSuper / 8)) continue;
-            const bool in = seg + 8 * u < K;
-            const uint32_t hw[4] = {xa[t].x, xa[t].y, xa[t].z, xa[t].w};
-            uint64_t v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t h = (hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-                nonfinite |= in && ((h >> 10) & 31u) == 31u;
-                v[i] = in ? biased_fixed(h) : kDigitBias;
-            }
-            const int p = u >> 4, rr = (u & 15) * 8;         // superchunk, k offset in it
-            const int gg = rr >> 5, m = (rr >> 4) & 1, h = (rr >> 3) & 1;
-            uint8_t* dst = table + p * kSuperBytes + ((m * 4 + gg) * kDigits) * 16 + 8 * h;
-#pragma unroll
-            for (int j = 0; j < kDigits; ++j) {
-                uint2 pair;
-                pair.x = digit_dword(v, 0, j);               // k offsets 0, 2, 4, 6
-                pair.y = digit_dword(v, 1, j);               // k offsets 1, 3, 5, 7
-                *reinterpret_cast<uint2*>(dst + 16 * j) = pair;
-            }
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t h = (hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+            nonfinite |= in && ((h >> 10) & 31u) == 31u;
+            v[i] = in ? biased_fixed(h) : kDigitBias;
         }
-        __syncthreads();
-
+        const int p = u >> 4, rr = (u & 15) * 8;             // superchunk, k offset in it
+        const int gg = rr >> 5, m = (rr >> 4) & 1, h = (rr >> 3) & 1;
+        uint8_t* dst = table + p * kSuperBytes + ((m * 4 + gg) * kDigits) * 16 + 8 * h;
 #pragma unroll
-        for (int i = 0; i < kMaxSuperPerWave; ++i) {
-            const int p = p0 + i;
+        for (int j = 0; j < kDigits; ++j) {
+            uint2 pair;
+            pair.x = digit_dword(v, 0, j);                   // k offsets 0, 2, 4, 6
+            pair.y = digit_dword(v, 1, j);                   // k offsets 1, 3, 5, 7
+            *reinterpret_cast<uint2*>(dst + 16 * j) = pair;
+        }
+    };
+    auto multiply = [&](int seg, const u4 (&wq)[kPerWave]) {
+        int nsc, per;
+        shape(seg, nsc, per);
+#pragma unroll
+        for (int i = 0; i < kPerWave; ++i) {
+            const int p = wave * per + i;
             if (i >= per || p >= nsc) break;
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
@@ -193,6 +196,23 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
             }
         }
+    };
+
+    u4 xa0, xa1;
+    u4 wq0[kPerWave], wq1[kPerWave];
+    if (K > 0) issue(0, xa0, wq0);
+    for (int seg = 0; seg < K; seg += 2 * kSeg) {
+        __syncthreads();                                     // earlier table reads are done
+        build(seg, xa0);
+        __syncthreads();
+        if (seg + kSeg < K) issue(seg + kSeg, xa1, wq1);
+        multiply(seg, wq0);
+        if (seg + kSeg >= K) break;
+        __syncthreads();
+        build(seg + kSeg, xa1);
+        __syncthreads();
+        if (seg + 2 * kSeg < K) issue(seg + 2 * kSeg, xa0, wq0);
+        multiply(seg + kSeg, wq1);
     }
 
     if (r < kDigits) {
@@ -267,7 +287,7 @@ extern "C" int w4a16_gemv(const int32_t* W, const uint16_t* A, const uint16_t* s
     const bool xvec = reinterpret_cast<uintptr_t>(A) % 16 == 0;
     auto kernel = wvec ? (xvec ? gemv_kernel<true, true> : gemv_kernel<true, false>)
                        : (xvec ? gemv_kernel<false, true> : gemv_kernel<false, false>);
-    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, reinterpret_cast<const uint32_t*>(W), A, sW, zW, C, (int)N,
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, st, reinterpret_cast<const uint32_t*>(W), A, sW, zW, C, (int)N,
                        (int)K);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
