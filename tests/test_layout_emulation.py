@@ -497,3 +497,25 @@ def test_group_prefill_x_rows_b_operand(M, TM):
                                 k = (c0 + cc) * 64 + 32 * h + 8 * c + 2 * kb
                                 assert lds[a] == (x[tok, k], x[tok, k + 1])
                             assert len(banks) == 64
+
+
+@pytest.mark.parametrize("tiles_m,tiles_n", [(16, 112), (16, 24), (3, 5), (1, 7), (5, 1), (9, 13), (16, 16)])
+@pytest.mark.parametrize("group_m", [1, 2, 3, 4, 8, 16])
+def test_wide_prefill_grouped_tile_order_is_a_bijection(tiles_m, tiles_n, group_m):
+    """prefill_wide_kernel's block -> (tm, tn) map (XCD remap, then groups of group_m M tiles with
+    the M tile fastest) visits every output tile exactly once."""
+    G = tiles_m * tiles_n
+    group_m = min(group_m, tiles_m)                  # as the launcher clamps it
+    G8 = G >> 3
+    seen = set()
+    for b in range(G):
+        tile = (b & 7) * G8 + (b >> 3) if b < (G8 << 3) else b
+        tn_count = G // tiles_m
+        gid = tile // (group_m * tn_count)
+        first_m = gid * group_m
+        gsz = min(tiles_m - first_m, group_m)
+        rem = tile - gid * group_m * tn_count
+        tm, tn = first_m + rem % gsz, rem // gsz
+        assert 0 <= tm < tiles_m and 0 <= tn < tiles_n
+        seen.add((tm, tn))
+    assert len(seen) == G
