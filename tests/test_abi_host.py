@@ -169,7 +169,8 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
 
 @pytest.mark.parametrize("M,N,K,want", [
     (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
-    (2048, 14336, 4096, 7),                                                  # partial last round: 128x128
+    (2048, 14336, 4096, 5), (1024, 6144, 4096, 5),                          # >= 3/4 of the CUs: 128x256
+    (1024, 4096, 4096, 7), (1024, 4096, 14336, 7),                           # 128 tiles of 128x256: 128x128
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
     (17, 4096, 14336, 17), (32, 6144, 4096, 17), (32, 14336, 4096, 17),     # token groups of 16
     (33, 4096, 4096, 17), (64, 4096, 4096, 17), (128, 4096, 14336, 17), (48, 14336, 4096, 17),

@@ -69,16 +69,12 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     int best = 0;
     double best_cost = std::numeric_limits<double>::infinity();
     const double cus = lim.cu_count > 0 ? lim.cu_count : 1;
-    // Large problems: the wide-tile kernels, when their tiles give every CU at least two rounds
-    // of full occupancy, in the order measured fastest on MI355X: 128 x 256 tiles (one workgroup
-    // per CU) when they fill whole rounds exactly, else 128 x 128 tiles of 2 waves (two per CU,
-    // shorter tails), then 128 x 256, then 256 x 128.
-    auto wide_tiles = [&](int cfg, int& occ) {
-        occ = prefill_occupancy(cfg, lim);
-        if (occ < 1 || !prefill_shape_ok(cfg, M, K)) return -1.0;
+    // Tiles of a wide-tile config, or -1 when it does not fit the device or the shape.
+    auto wide_tiles = [&](int cfg) {
+        if (prefill_occupancy(cfg, lim) < 1 || !prefill_shape_ok(cfg, M, K)) return -1.0;
         const PrefillTile& t = kPrefillTable[cfg];
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
-        return tiles >= 2.0 * cus * occ && tiles <= (double)std::numeric_limits<int32_t>::max() ? tiles : -1.0;
+        return tiles <= (double)std::numeric_limits<int32_t>::max() ? tiles : -1.0;
     };
     // Rules measured on MI355X (graph-timed sweep of every config over M = 17..1024 on the
     // Llama-3-8B projection shapes):
@@ -96,7 +92,12 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //  * token groups of 64 rows while those waves are at most 8 per CU (N = 4096, M = 512: 43 vs
     //    46 us; N = 28672, M = 64: 45 vs 50 us);
     //  * then the wide tiles, which beat the 16..128-row tiles for every larger size measured
-    //    (N = 6144, M = 512: 54 vs 73 us).
+    //    (N = 6144, M = 512: 54 vs 73 us): 128 x 256 tiles (two workgroups per CU) once they
+    //    number at least 3/4 of the CUs, else 128 x 128 tiles.  Forced-config sweep, K = 4096
+    //    unless noted: 128 x 256 vs 128 x 128 at N = 6144, M = 1024 (192 tiles): 62.2 vs 66.6 us;
+    //    M = 2048: 116.1 vs 129.5; N = 28672, M = 512: 133.2 vs 139.9, M = 1024: 245.0 vs 269.0;
+    //    N = 4096, M = 2048: 73.9 vs 78.6; at 128 tiles 128 x 128 wins (N = 4096, M = 1024: 57.9
+    //    vs 53.7 us; K = 14336: 183.3 vs 170.5).  256 x 128 tiles lost everywhere.
     const double blocks = std::ceil(N / 16.0);
     if (prefill_occupancy(17, lim) > 0 && prefill_shape_ok(17, M, K) &&
         std::ceil(M / 16.0) * blocks <= 12.0 * cus)
@@ -112,14 +113,8 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     if (prefill_occupancy(11, lim) > 0 && prefill_shape_ok(11, M, K) &&
         std::ceil(M / 64.0) * blocks <= 8.0 * cus)
         return 11;
-    int occ5 = 0;
-    const double t5 = wide_tiles(5, occ5);
-    if (t5 > 0 && std::fmod(t5, cus * occ5) == 0.0) return 5;
-    for (int cfg : {7, 5, 6}) {
-        int occ = 0;
-        if (wide_tiles(cfg, occ) > 0) return cfg;
-    }
-    if (prefill_occupancy(7, lim) > 0 && prefill_shape_ok(7, M, K)) return 7;
+    if (wide_tiles(5) >= 0.75 * cus) return 5;
+    if (wide_tiles(7) > 0) return 7;
     for (int cfg = kNumPrefillTable; cfg >= 1; --cfg) {    // descending: ties go to the later config
         const int occ = prefill_occupancy(cfg, lim);
         if (occ < 1 || !prefill_shape_ok(cfg, M, K) || kPrefillTable[cfg].kind >= 1) continue;   // other kinds: rules above
