@@ -225,8 +225,10 @@ def bench_gemv(torch, steps, warmup):
         us = ms * 1e3 / (steps * copies)
         gbs = gemv_bytes(N, K) / (us * 1e-6) / 1e9
         log(f"gemv {name} N={N} K={K}: {us:.2f} us  {gbs:.0f} GB/s")
+        rt = 2 if -(-N // 32) >= torch.cuda.get_device_properties(0).multi_processor_count else 1
         cases.append({"layer": name, "N": N, "K": K, "us": round(us, 3), "GBps": round(gbs, 1),
-                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": copies})
+                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": copies,
+                      "kernel": f"w4a16::gemv_kernel<true, true, {rt}>"})
         del Ws, g
     total_b = sum(gemv_bytes(c["N"], c["K"]) for c in cases)
     total_us = sum(c["us"] for c in cases)
@@ -435,7 +437,7 @@ def main(argv=None) -> int:
                           "timing": "HIP graph replay over rotating weight copies, HIP events"},
                "roofline": {"bound": "hbm", "achieved": round(gv["value"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(gv["value"] / HBM_PEAK_GBS, 4), "traffic": load_traffic("gemv"),
-                            "kernel": "w4a16::gemv_kernel<true, true>",
+                            "kernel": " + ".join(sorted({c["kernel"] for c in gv["cases"]})),
                             "bytes_per_launch": gv["bytes_per_launch"],
                             "avg_launch_us": round(gv["avg_launch_us"], 3)},
                "cases": gv["cases"]}
@@ -506,7 +508,7 @@ def main(argv=None) -> int:
         out["baseline_gemv"] = {"value": round(gv["value"], 1), "unit": "GB/s",
                                 "frac_hbm": round(gv["value"] / HBM_PEAK_GBS, 4),
                                 "us_per_step": round(gv["us_per_step"], 2), "cases": gv["cases"],
-                                "kernel": "w4a16::gemv_kernel<true, true>"}
+                                "kernel": " + ".join(sorted({c["kernel"] for c in gv["cases"]}))}
     if not a.no_cpu:
         if dec is not None:
             out["cpu_baseline"] = cpu_baseline(DECODE_CASES)

@@ -223,7 +223,7 @@ def test_signed_nibble_bytes():
                 assert np.array_equal(sb[v, j], want), (shift, j, v)
 
 
-def emulate_gemv_kernel(W, A, N, K, wvec):
+def emulate_gemv_kernel(W, A, N, K, wvec, rt=1):
     """Digit sums P[n, j] of one launch, following gemv_kernel's indexing exactly: the A loads of
     the table build, each lane's weight-load word indices (checked in bounds), the digit table,
     the operand bytes and a 16x16x64 MFMA (A and B use the same k position for the same lane
@@ -232,9 +232,9 @@ def emulate_gemv_kernel(W, A, N, K, wvec):
     Wu = W.view(np.uint32)
     h_all = A.view(np.uint16)
     P = np.zeros((N, DIGITS), dtype=object)
-    for row0 in range(0, N, 16):
-        rows = [min(row0 + r, N - 1) for r in range(16)]
-        acc = np.zeros((WAVES, 16, 16), dtype=np.int64)        # per wave: [row, column]
+    for row0 in range(0, N, 16 * rt):
+        rows = [min(row0 + 16 * t + r, N - 1) for t in range(rt) for r in range(16)]
+        acc = np.zeros((WAVES, 16 * rt, 16), dtype=np.int64)   # per wave: [row, column]
         for seg in range(0, K, SEG):
             seglen = min(SEG, K - seg)
             nsc = (seglen + SUPER - 1) // SUPER
@@ -263,7 +263,7 @@ def emulate_gemv_kernel(W, A, N, K, wvec):
                     p_load = wave * per + min(i, per - 1)          # loads past the share repeat
                     lanes_words = {}
                     for g in range(4):
-                        for r in range(16):
+                        for r in range(16 * rt):                   # row tile r // 16, lane row r % 16
                             wi = ((seg + p_load * SUPER) >> 3) + 4 * g
                             if wvec:
                                 idx = [wi + e for e in range(4)] if wi + 4 <= kw else [e for e in range(4)]
@@ -274,10 +274,10 @@ def emulate_gemv_kernel(W, A, N, K, wvec):
                     if i >= per or p >= nsc:
                         break
                     for m in range(2):
-                        Abytes = np.zeros((16, 4, 16), dtype=np.int64)       # [row r, group g, byte]
+                        Abytes = np.zeros((16 * rt, 4, 16), dtype=np.int64)  # [row r, group g, byte]
                         Bbytes = np.zeros((16, 4, 16), dtype=np.int64)       # [column r, group g, byte]
                         for g in range(4):
-                            for r in range(16):
+                            for r in range(16 * rt):
                                 w = lanes_words[(r, g)]
                                 w0, w1 = (w[2], w[3]) if m else (w[0], w[1])
                                 dws = []
@@ -286,24 +286,25 @@ def emulate_gemv_kernel(W, A, N, K, wvec):
                                         uu = ((ww ^ 0x88888888) >> shift) & 0x0F0F0F0F
                                         dws.append(((uu + 0x78787878) ^ 0x80808080) & 0xFFFFFFFF)
                                 Abytes[r, g] = np.array(dws, dtype=np.uint32).view(np.int8)
-                                if r < DIGITS:
+                                if r < DIGITS and r < 16:
                                     off = p * 768 + ((m * 4 + g) * DIGITS + r) * 16
                                     tb = table[off:off + 16]
                                     assert not (tb == 0xEE).all(), "read of an unwritten table entry"
                                     Bbytes[r, g] = tb.view(np.int8)
                         acc[wave] += np.einsum("rgb,cgb->rc", Abytes, Bbytes)
-        for r in range(16):
+        for r in range(16 * rt):
             if row0 + r < N:
                 for j in range(DIGITS):
                     P[row0 + r, j] = int(acc[:, r, j].sum())
     return P
 
 
-@pytest.mark.parametrize("N,K,wvec", [(16, 512, True), (13, 4096 + 384, True), (5, 1032, False),
-                                      (3, 8, False), (17, 160, True)])
-def test_gemv_kernel_index_math_emulated(N, K, wvec):
+@pytest.mark.parametrize("N,K,wvec,rt", [(16, 512, True, 1), (13, 4096 + 384, True, 1), (5, 1032, False, 1),
+                                         (3, 8, False, 1), (17, 160, True, 1), (40, 640, True, 2),
+                                         (29, 1032, False, 2), (32, 4096 + 128, True, 2)])
+def test_gemv_kernel_index_math_emulated(N, K, wvec, rt):
     W, A, _, _ = make_gemv(N, K, 21, special=True)
-    P = emulate_gemv_kernel(W, A, N, K, wvec)
+    P = emulate_gemv_kernel(W, A, N, K, wvec, rt)
     wv = signed_nibbles(W, K)
     X = [int(float(a) * 2**24) for a in A.astype(np.float64)]
     for n in range(N):
@@ -391,7 +392,8 @@ def test_gemv_bit_exact_vs_oracle(N, K):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("N,K,w_off,a_off", [(64, 4096, 1, 0), (64, 4096, 0, 1), (33, 1024, 2, 3), (40, 520, 1, 1)])
+@pytest.mark.parametrize("N,K,w_off,a_off", [(64, 4096, 1, 0), (64, 4096, 0, 1), (33, 1024, 2, 3), (40, 520, 1, 1),
+                                             (8200, 1032, 1, 0), (8224, 136, 0, 1), (8208, 4104, 0, 0)])
 def test_gemv_misaligned_operands(N, K, w_off, a_off):
     print(f"gemv misaligned N={N} K={K} w_off={w_off} a_off={a_off}", flush=True)
     W, A, sW, zW = make_gemv(N, K, 2, special=True)

@@ -20,7 +20,7 @@
 // order: a NaN term, 0 * inf, or +inf together with -inf give NaN, otherwise any infinite term
 // gives that infinity.
 //
-// Workgroup = 8 waves on 16 rows.  K is processed in segments of 4096: each of the 512 threads
+// Workgroup = 8 waves on 16 or 32 rows.  K is processed in segments of 4096: each of the 512 threads
 // converts 8 A values into the digit table in LDS (laid out as the B operands), then each wave
 // multiplies a contiguous eighth of the segment's 128-wide superchunks.  Lane (r, g) = (lane %
 // 16, lane / 16) loads 16 bytes of row r per superchunk: the 32 weights at k = 128p + 32g .. +31,
@@ -28,6 +28,8 @@
 // waves (row 4g + i, digit r in lane (r, g), element i) are summed in LDS (exact integers).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "w4a16.h"
 #include "w4a16_device.h"
@@ -39,7 +41,7 @@ namespace {
 
 typedef int32_t i4v __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 16;                  // rows per workgroup (one MFMA row tile)
+constexpr int kRows = 16;                  // rows per MFMA row tile
 constexpr int kWaves = 8;                  // waves per workgroup, splitting each segment's k range
 constexpr int kThreads = kWaves * 64;
 constexpr int kSeg = 4096;                 // k per digit-table segment
@@ -52,20 +54,44 @@ constexpr uint64_t kDigitBias = 0x808080808080ull;  // 128 * sum_j 256^j
 static_assert(kSeg % (kSuper * kWaves) == 0, "segment must split evenly over the waves");
 static_assert(kSeg / 8 == kThreads, "the table build gives each thread one 8-k unit");
 
-// a * 2^24 + kDigitBias for a finite fp16 a (non-finite values give kDigitBias, i.e. X = 0).
+// a * 2^24 + kDigitBias for a finite fp16 a (callers pass 0 for inputs that must count as 0).
+// Branch-free: the mantissa with its hidden bit is shifted by max(e, 1) - 1, and the sign is
+// applied as (mag ^ s) - s with s = 0 or -1.
 __device__ __forceinline__ uint64_t biased_fixed(uint32_t h) {
-    const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
-    const uint64_t mag = e == 0 ? (uint64_t)m : (uint64_t)(1024u | m) << (e - 1);
-    const uint64_t v = (h & 0x8000u) ? kDigitBias - mag : kDigitBias + mag;
-    return e == 31 ? kDigitBias : v;
+    const uint32_t e = (h >> 10) & 31u;
+    const uint32_t mant = (h & 1023u) | (e != 0 ? 1024u : 0u);
+    const uint64_t mag = (uint64_t)mant << (max(e, 1u) - 1u);
+    const uint64_t sgn = (uint64_t)(-(int64_t)((h >> 15) & 1u));
+    return ((mag ^ sgn) - sgn) + kDigitBias;
 }
 
-// Digit j (as a signed byte in two's complement) of four biased values, packed little-endian.
-__device__ __forceinline__ uint32_t digit_dword(const uint64_t (&v)[8], int first, int j) {
-    uint32_t d = 0;
+// 4x4 byte transpose: out[j] byte i = byte j of in[i] (v_perm_b32 picks bytes of {src0, src1},
+// selector values 0..3 = src1, 4..7 = src0).
+__device__ __forceinline__ void byte_transpose(const uint32_t (&in)[4], uint32_t (&out)[4]) {
+    const uint32_t u01l = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);
+    const uint32_t u01h = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);
+    const uint32_t u23l = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+    const uint32_t u23h = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+    out[0] = __builtin_amdgcn_perm(u23l, u01l, 0x05040100u);
+    out[1] = __builtin_amdgcn_perm(u23l, u01l, 0x07060302u);
+    out[2] = __builtin_amdgcn_perm(u23h, u01h, 0x05040100u);
+    out[3] = __builtin_amdgcn_perm(u23h, u01h, 0x07060302u);
+}
+
+// Digit dwords of four biased values: d[j] byte i = digit j of value i as a signed byte
+// (the byte of X + kDigitBias minus 128, i.e. XOR 0x80), j = 0..5.
+__device__ __forceinline__ void digit_dwords(const uint64_t (&v)[4], uint32_t (&d)[kDigits]) {
+    const uint32_t lo[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+    uint32_t t[4];
+    byte_transpose(lo, t);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d |= (uint32_t)((v[first + 2 * i] >> (8 * j)) & 0xFFu) << (8 * i);
-    return d ^ 0x80808080u;
+    for (int j = 0; j < 4; ++j) d[j] = t[j] ^ 0x80808080u;
+    const uint32_t h0 = (uint32_t)(v[0] >> 32), h1 = (uint32_t)(v[1] >> 32);
+    const uint32_t h2 = (uint32_t)(v[2] >> 32), h3 = (uint32_t)(v[3] >> 32);
+    const uint32_t v01 = __builtin_amdgcn_perm(h1, h0, 0x05010400u);
+    const uint32_t v23 = __builtin_amdgcn_perm(h3, h2, 0x05010400u);
+    d[4] = __builtin_amdgcn_perm(v23, v01, 0x05040100u) ^ 0x80808080u;
+    d[5] = __builtin_amdgcn_perm(v23, v01, 0x07060302u) ^ 0x80808080u;
 }
 
 // Signed bytes of the even (shift 0) or odd (shift 4) nibbles of a word: nibble n becomes
@@ -100,20 +126,27 @@ __device__ int nonfinite_class(const uint32_t* __restrict__ wrow, const uint16_t
 // Segments are double-buffered: the A values and weights of segment s + 1 are requested before
 // the MFMAs of segment s, so their latency overlaps that work.  Every load is issued
 // unconditionally (clamped addresses) so the compiler's waits count exactly the loads in flight.
-template <bool WVEC, bool XVEC>
+// RT: row tiles of 16 per workgroup.  Each digit-table B operand feeds RT MFMAs, so the A
+// conversion (done once per workgroup and segment) is shared by 16 RT rows.
+template <bool WVEC, bool XVEC, int RT>
 __global__ void __launch_bounds__(kThreads)
 gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, const uint16_t* __restrict__ sW,
             const uint16_t* __restrict__ zW, uint16_t* __restrict__ C, int N, int K) {
+    constexpr int ROWS = kRows * RT;
     __shared__ __align__(16) uint8_t table[kSeg / kSuper * kSuperBytes];
-    __shared__ int32_t part[kWaves][kRows][8];
+    __shared__ int32_t part[kWaves][ROWS][8];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int row0 = blockIdx.x * kRows;
+    const int row0 = blockIdx.x * ROWS;
     const int kw = K >> 3;                                   // words per row
-    const uint32_t* __restrict__ wrow = W + (size_t)min(row0 + r, N - 1) * kw;
-    i4v acc = {0, 0, 0, 0};
+    const uint32_t* __restrict__ wrow[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) wrow[t] = W + (size_t)min(row0 + kRows * t + r, N - 1) * kw;
+    i4v acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = i4v{0, 0, 0, 0};
     int nonfinite = 0;
 
     // superchunks of segment `seg`, and this wave's share (a contiguous range starting at p0)
@@ -122,7 +155,7 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
         per = (nsc + kWaves - 1) / kWaves;
     };
     // Request the A values of this thread's 8-k unit and this wave's weights for segment `seg`.
-    auto issue = [&](int seg, u4& xa, u4 (&wq)[kPerWave]) {
+    auto issue = [&](int seg, u4& xa, u4 (&wq)[RT][kPerWave]) {
         int nsc, per;
         shape(seg, nsc, per);
         const int k0 = seg + 8 * tid;
@@ -139,13 +172,16 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
         for (int i = 0; i < kPerWave; ++i) {
             const int p = wave * per + min(i, per - 1);      // past the share: repeat its last one
             const int wi = ((seg + p * kSuper) >> 3) + 4 * g;   // first word of the lane's 32 weights
-            if constexpr (WVEC) {
-                wq[i] = *reinterpret_cast<const u4*>(wrow + (wi + 4 <= kw ? wi : 0));
-            } else {
-                uint32_t d[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) d[e] = wrow[wi + e < kw ? wi + e : 0];
-                wq[i] = u4{d[0], d[1], d[2], d[3]};
+            for (int t = 0; t < RT; ++t) {
+                if constexpr (WVEC) {
+                    wq[t][i] = *reinterpret_cast<const u4*>(wrow[t] + (wi + 4 <= kw ? wi : 0));
+                } else {
+                    uint32_t d[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) d[e] = wrow[t][wi + e < kw ? wi + e : 0];
+                    wq[t][i] = u4{d[0], d[1], d[2], d[3]};
+                }
             }
         }
     };
@@ -157,26 +193,26 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
         const int u = tid;
         if (u >= nsc * (kSuper / 8)) return;
         const bool in = seg + 8 * u < K;
-        const uint32_t hw[4] = {xa.x, xa.y, xa.z, xa.w};
-        uint64_t v[8];
+        const uint32_t hw[4] = {in ? xa.x : 0u, in ? xa.y : 0u, in ? xa.z : 0u, in ? xa.w : 0u};
+        uint64_t ve[4], vo[4];                               // k offsets 0, 2, 4, 6 and 1, 3, 5, 7
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t h = (hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-            nonfinite |= in && ((h >> 10) & 31u) == 31u;
-            v[i] = in ? biased_fixed(h) : kDigitBias;
+            uint32_t h = (hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+            const bool special = ((h >> 10) & 31u) == 31u;   // inf / NaN: counted as 0 here
+            nonfinite |= special;
+            h = special ? 0u : h;
+            (i & 1 ? vo : ve)[i >> 1] = biased_fixed(h);
         }
+        uint32_t de[kDigits], dd[kDigits];
+        digit_dwords(ve, de);
+        digit_dwords(vo, dd);
         const int p = u >> 4, rr = (u & 15) * 8;             // superchunk, k offset in it
         const int gg = rr >> 5, m = (rr >> 4) & 1, h = (rr >> 3) & 1;
         uint8_t* dst = table + p * kSuperBytes + ((m * 4 + gg) * kDigits) * 16 + 8 * h;
 #pragma unroll
-        for (int j = 0; j < kDigits; ++j) {
-            uint2 pair;
-            pair.x = digit_dword(v, 0, j);                   // k offsets 0, 2, 4, 6
-            pair.y = digit_dword(v, 1, j);                   // k offsets 1, 3, 5, 7
-            *reinterpret_cast<uint2*>(dst + 16 * j) = pair;
-        }
+        for (int j = 0; j < kDigits; ++j) *reinterpret_cast<uint2*>(dst + 16 * j) = uint2{de[j], dd[j]};
     };
-    auto multiply = [&](int seg, const u4 (&wq)[kPerWave]) {
+    auto multiply = [&](int seg, const u4 (&wq)[RT][kPerWave]) {
         int nsc, per;
         shape(seg, nsc, per);
 #pragma unroll
@@ -185,21 +221,24 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
             if (i >= per || p >= nsc) break;
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
-                const uint32_t w0 = m ? wq[i].z : wq[i].x, w1 = m ? wq[i].w : wq[i].y;
-                const i4v a = {(int32_t)signed_nibbles(w0, 0), (int32_t)signed_nibbles(w0, 4),
-                               (int32_t)signed_nibbles(w1, 0), (int32_t)signed_nibbles(w1, 4)};
                 i4v b = {0, 0, 0, 0};
                 if (r < kDigits) {
                     const u4 t = *reinterpret_cast<const u4*>(table + p * kSuperBytes + ((m * 4 + g) * kDigits + r) * 16);
                     b = i4v{(int32_t)t.x, (int32_t)t.y, (int32_t)t.z, (int32_t)t.w};
                 }
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < RT; ++t) {
+                    const uint32_t w0 = m ? wq[t][i].z : wq[t][i].x, w1 = m ? wq[t][i].w : wq[t][i].y;
+                    const i4v a = {(int32_t)signed_nibbles(w0, 0), (int32_t)signed_nibbles(w0, 4),
+                                   (int32_t)signed_nibbles(w1, 0), (int32_t)signed_nibbles(w1, 4)};
+                    acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+                }
             }
         }
     };
 
     u4 xa0, xa1;
-    u4 wq0[kPerWave], wq1[kPerWave];
+    u4 wq0[RT][kPerWave], wq1[RT][kPerWave];
     if (K > 0) issue(0, xa0, wq0);
     for (int seg = 0; seg < K; seg += 2 * kSeg) {
         __syncthreads();                                     // earlier table reads are done
@@ -217,10 +256,12 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
 
     if (r < kDigits) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part[wave][4 * g + i][r] = acc[i];
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) part[wave][kRows * t + 4 * g + i][r] = acc[t][i];
     }
     const bool any_nonfinite = __syncthreads_or(nonfinite);
-    if (tid < kRows && row0 + tid < N) {
+    if (tid < ROWS && row0 + tid < N) {
         const int n = row0 + tid;
         int64_t total = 0;
 #pragma unroll
@@ -282,11 +323,23 @@ extern "C" int w4a16_gemv(const int32_t* W, const uint16_t* A, const uint16_t* s
         return W4A16_ERR_INVALID;
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)((N + kRows - 1) / kRows));
+    // Two row tiles per workgroup once that still gives every CU a workgroup (N = 14336, K = 4096:
+    // 448 workgroups, 10.8 -> 9.9 us); one otherwise, so a small N still keeps every CU busy.
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        w4a16_device_limits lim;
+        if (w4a16_query_device(dev, &lim) == W4A16_OK && lim.cu_count > 0) cus = lim.cu_count;
+    }
+    const bool two = (N + 2 * kRows - 1) / (2 * kRows) >= cus;
+    const dim3 grid((unsigned)((N + (two ? 2 : 1) * kRows - 1) / ((two ? 2 : 1) * kRows)));
     const bool wvec = reinterpret_cast<uintptr_t>(W) % 16 == 0 && K % 32 == 0;
     const bool xvec = reinterpret_cast<uintptr_t>(A) % 16 == 0;
-    auto kernel = wvec ? (xvec ? gemv_kernel<true, true> : gemv_kernel<true, false>)
-                       : (xvec ? gemv_kernel<false, true> : gemv_kernel<false, false>);
+    auto pick = [&](auto rt) {
+        constexpr int R = decltype(rt)::value;
+        return wvec ? (xvec ? gemv_kernel<true, true, R> : gemv_kernel<true, false, R>)
+                    : (xvec ? gemv_kernel<false, true, R> : gemv_kernel<false, false, R>);
+    };
+    auto kernel = two ? pick(std::integral_constant<int, 2>{}) : pick(std::integral_constant<int, 1>{});
     hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, st, reinterpret_cast<const uint32_t*>(W), A, sW, zW, C, (int)N,
                        (int)K);
     const hipError_t e = hipGetLastError();
