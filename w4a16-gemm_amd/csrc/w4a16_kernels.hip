@@ -17,6 +17,11 @@
 
 namespace w4a16 {
 
+// Cache policy of the decode kernels' weight DMAs: nontemporal (`nt`), since a decode call reads
+// every weight byte exactly once (aux operand of __builtin_amdgcn_global_load_lds: 1 = sc0,
+// 2 = nt, 16 = sc1 on gfx950).
+constexpr int kWeightStreamPolicy = 2;
+
 // ------------------------------------------------------------------------------------ decode
 // Replaces the reference decode kernel w4a16_gemm_mma (src/vectorized/decode.cuh:18-159).
 //
@@ -253,7 +258,7 @@ decode_lds_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         for (int b = 0; b < NBW; ++b) {
             const u4* src = Wp + ((size_t)(nb0 + b) * KC + kc0 + 2 * p) * 32 + lane;
             auto* dst = (__attribute__((address_space(3))) void*)(wreg + (b * NPAIR + p) * 1024);
-            if (2 * p + 1 < KCW || lane < 32) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+            if (2 * p + 1 < KCW || lane < 32) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, kWeightStreamPolicy);
         }
     asm volatile("" ::: "memory");
 
@@ -365,7 +370,7 @@ decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
         for (int b = 0; b < NBW; ++b) {
             auto* dst = (__attribute__((address_space(3))) void*)(wreg + slot * SLOT + b * 1024);
-            __builtin_amdgcn_global_load_lds(wsrc + (size_t)b * KC * 32 + (size_t)c * 32, dst, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(wsrc + (size_t)b * KC * 32 + (size_t)c * 32, dst, 16, 0, kWeightStreamPolicy);
         }
         asm volatile("" ::: "memory");
     };
@@ -545,7 +550,8 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
         for (int b = 0; b < NBW; ++b)
             __builtin_amdgcn_global_load_lds((const void*)(wbase_g + (size_t)b * KC * 512 + (size_t)p * (1024 * WAVES) + woff_g),
-                                             (__attribute__((address_space(3))) void*)(sl + b * 1024), 16, 0, 0);
+                                             (__attribute__((address_space(3))) void*)(sl + b * 1024), 16, 0,
+                                             kWeightStreamPolicy);
         if constexpr (XR == 1) {
             __builtin_amdgcn_global_load_lds((const void*)(xsrc[0] + (size_t)p * (256 * WAVES)),
                                              (__attribute__((address_space(3))) void*)(sl + WSLOT), 4, 0, 0);
