@@ -197,8 +197,9 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             //    rings of 4 waves, 2 blocks while the x rows are few (M <= 4), else 4 blocks; no
             //    split;
             //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves,
-            //    3 pairs in flight up to 4 token rows and 2 up to 8 rows (two-block tiles split in
-            //    two above 8 rows, where the x traffic per block grows);
+            //    3 pairs in flight up to 4 token rows and 2 up to 8 rows; above 8 rows, where the x
+            //    traffic per block grows, two-block tiles of 4 waves split in two (M = 16: 11.95
+            //    vs 12.57 us for 8 waves, in two sweeps);
             //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves.
             auto ok = [&](int cand, int sp) {
                 return decode_shape_fits(cand, KC, sp, G) && decode_lds_bytes(cand, M) <= lim->lds_bytes_per_block &&
@@ -210,7 +211,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             Cand wide[] = {{24, 1}, {20, 1}, {7, 1}};
             Cand longk_m4[] = {{37, 1}, {27, 1}, {30, 2}};
             Cand longk_small_m[] = {{27, 1}, {30, 2}, {30, 2}};
-            Cand longk_large_m[] = {{30, 2}, {27, 1}, {27, 1}};
+            Cand longk_large_m[] = {{28, 2}, {30, 2}, {27, 1}};
             Cand shortk_m1[] = {{37, 1}, {27, 1}, {22, 1}};
             Cand shortk[] = {{27, 1}, {29, 1}, {29, 1}};
             Cand* list;
