@@ -55,14 +55,17 @@ static_assert(kSeg % (kSuper * kWaves) == 0, "segment must split evenly over the
 static_assert(kSeg / 8 == kThreads, "the table build gives each thread one 8-k unit");
 
 // a * 2^24 + kDigitBias for a finite fp16 a (callers pass 0 for inputs that must count as 0).
-// Branch-free: the mantissa with its hidden bit is shifted by max(e, 1) - 1, and the sign is
-// applied as (mag ^ s) - s with s = 0 or -1.
+// Branch-free: the hidden bit is min(e, 1), the mantissa is shifted by e - min(e, 1), and the
+// sign is applied as (mag ^ s) - s = (mag ^ s) + (s & 1) with s = 0 or all ones, folded into the
+// bias.
 __device__ __forceinline__ uint64_t biased_fixed(uint32_t h) {
     const uint32_t e = (h >> 10) & 31u;
-    const uint32_t mant = (h & 1023u) | (e != 0 ? 1024u : 0u);
-    const uint64_t mag = (uint64_t)mant << (max(e, 1u) - 1u);
-    const uint64_t sgn = (uint64_t)(-(int64_t)((h >> 15) & 1u));
-    return ((mag ^ sgn) - sgn) + kDigitBias;
+    const uint32_t hid = min(e, 1u);
+    const uint32_t mant = (h & 1023u) | (hid << 10);
+    const uint64_t mag = (uint64_t)mant << (e - hid);
+    const uint32_t s = 0u - ((h >> 15) & 1u);
+    const uint64_t sx = ((uint64_t)s << 32) | s;
+    return (mag ^ sx) + (kDigitBias + (s & 1u));
 }
 
 // 4x4 byte transpose: out[j] byte i = byte j of in[i] (v_perm_b32 picks bytes of {src0, src1},
@@ -193,16 +196,27 @@ gemv_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ A, cons
         const int u = tid;
         if (u >= nsc * (kSuper / 8)) return;
         const bool in = seg + 8 * u < K;
-        const uint32_t hw[4] = {in ? xa.x : 0u, in ? xa.y : 0u, in ? xa.z : 0u, in ? xa.w : 0u};
+        uint32_t hw[4] = {in ? xa.x : 0u, in ? xa.y : 0u, in ? xa.z : 0u, in ? xa.w : 0u};
+        // inf / NaN count as 0 here (their class is applied in the epilogue); rare, so one test
+        // per 8 values and the zeroing behind a branch
+        bool special = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t ee = hw[q] & 0x7C007C00u;
+            special |= (ee & 0xFFFFu) == 0x7C00u || (ee >> 16) == 0x7C00u;
+        }
+        if (special) {
+            nonfinite = 1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t ee = hw[q] & 0x7C007C00u;
+                hw[q] &= ((ee & 0xFFFFu) == 0x7C00u ? 0xFFFF0000u : 0xFFFFFFFFu) &
+                         ((ee >> 16) == 0x7C00u ? 0x0000FFFFu : 0xFFFFFFFFu);
+            }
+        }
         uint64_t ve[4], vo[4];                               // k offsets 0, 2, 4, 6 and 1, 3, 5, 7
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            uint32_t h = (hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-            const bool special = ((h >> 10) & 31u) == 31u;   // inf / NaN: counted as 0 here
-            nonfinite |= special;
-            h = special ? 0u : h;
-            (i & 1 ? vo : ve)[i >> 1] = biased_fixed(h);
-        }
+        for (int i = 0; i < 8; ++i) (i & 1 ? vo : ve)[i >> 1] = biased_fixed((hw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
         uint32_t de[kDigits], dd[kDigits];
         digit_dwords(ve, de);
         digit_dwords(vo, dd);
