@@ -391,8 +391,8 @@ def main(argv=None) -> int:
     ap.add_argument("--json", default=None, help="also write the JSON line to this file")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU only (the op is single-GPU; see DESIGN.md for how "
-              "it would shard); use --gpus 1", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (the op runs on one GPU; several GPUs would shard "
+              "N column-parallel or K row-parallel); use --gpus 1", file=sys.stderr)
         return 2
 
     import torch
