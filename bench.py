@@ -228,7 +228,7 @@ def bench_gemv(torch, steps, warmup):
         rt = 2 if -(-N // 32) >= torch.cuda.get_device_properties(0).multi_processor_count else 1
         cases.append({"layer": name, "N": N, "K": K, "us": round(us, 3), "GBps": round(gbs, 1),
                       "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "copies": copies,
-                      "kernel": f"w4a16::gemv_kernel<true, true, {rt}>"})
+                      "kernel": f"w4a16::(anonymous namespace)::gemv_kernel<true, true, {rt}>"})
         del Ws, g
     total_b = sum(gemv_bytes(c["N"], c["K"]) for c in cases)
     total_us = sum(c["us"] for c in cases)

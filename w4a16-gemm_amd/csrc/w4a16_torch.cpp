@@ -13,6 +13,7 @@
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
+#include <initializer_list>
 #include <map>
 #include <mutex>
 
@@ -142,24 +143,29 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
     d["tile_n"] = plan.tile_n; d["grid"] = plan.grid; d["block"] = plan.block;
     d["counter_slots"] = plan.counter_slots; d["workspace_bytes"] = (uint64_t)plan.workspace_bytes;
     d["decode_variant"] = plan.decode_variant;
+    // Names as the compiler demangles them (what rocprofv3 reports), e.g.
+    // "w4a16::decode_ring_kernel<2, 4, 2, 1>".
+    auto tmpl = [](const char* name, std::initializer_list<int> args) {
+        std::string s = std::string("w4a16::") + name + "<";
+        bool first = true;
+        for (int a : args) { s += (first ? "" : ", ") + std::to_string(a); first = false; }
+        return s + ">";
+    };
     if (plan.kernel == W4A16_VARIANT_DECODE) {
         static const char* const kinds[] = {"decode_kernel", "decode_lds_kernel", "decode_stream_kernel",
                                             "decode_ring_kernel"};
         const w4a16::DecodeCfg& c = w4a16::kDecodeTable[plan.decode_variant];
-        d["kernel_name"] = std::string("w4a16::") + kinds[c.kind] + "<" + std::to_string(c.nbw) + "," +
-                           std::to_string(c.waves) + "," + std::to_string(c.d) + ">";
+        d["kernel_name"] = c.kind == 3 ? tmpl(kinds[3], {c.nbw, c.waves, c.d, w4a16::decode_ring_xr((int)M)})
+                                       : tmpl(kinds[c.kind], {c.nbw, c.waves, c.d});
     } else {
         const w4a16::PrefillTile& t = w4a16::kPrefillTable[plan.kernel];
-        static const char* const pk[] = {"w4a16::prefill_kernel<", "w4a16::prefill_wide_kernel<",
-                                         "w4a16::prefill_stream_kernel<", "w4a16::prefill_group_kernel<"};
         if (t.kind == 2)
-            d["kernel_name"] = std::string(pk[2]) + std::to_string(t.bm / 16) + "," + std::to_string(t.depth) + ">";
+            d["kernel_name"] = tmpl("prefill_stream_kernel", {t.bm / 16, t.depth});
         else if (t.kind == 3)
-            d["kernel_name"] = std::string(pk[3]) + std::to_string(t.bm / 16) + "," + std::to_string(t.depth) + "," +
-                               std::to_string(t.waves_n) + "," + std::to_string(t.bn / (16 * t.waves_n)) + ">";
+            d["kernel_name"] = tmpl("prefill_group_kernel", {t.bm / 16, t.depth, t.waves_n, t.bn / (16 * t.waves_n)});
         else
-        d["kernel_name"] = std::string(pk[t.kind]) + std::to_string(t.bm) + "," + std::to_string(t.bn) + "," +
-                           std::to_string(t.waves_m) + "," + std::to_string(t.waves_n) + ">";
+            d["kernel_name"] = tmpl(t.kind == 1 ? "prefill_wide_kernel" : "prefill_kernel",
+                                    {t.bm, t.bn, t.waves_m, t.waves_n});
     }
     d["cu_count"] = lim.cu_count; d["gcn_arch"] = lim.gcn_arch; d["lds_bytes_per_block"] = lim.lds_bytes_per_block;
     return d;
