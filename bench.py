@@ -50,7 +50,8 @@ DECODE_CASES = [("gate_up", 14336, 4096, m) for m in (1, 4, 8, 16)] + \
 PREFILL_CASE = ("mlp70b", 28672, 8192, 2048)
 MODERATE_CASE = ("gate_up", 14336, 4096, 128, 64)          # M=128, G=64
 GRAPH_STEPS = 12                                             # decode steps captured per graph
-GEMV_CASES = [("decode_c1", 4096, 4096), ("gate_up", 14336, 4096)]   # (name, N, K) of w4a16_ext.w4a16_gemv
+GEMV_CASES = [("c1_shape", 4096, 4096), ("gate_up", 14336, 4096)]    # (name, N, K) of w4a16_ext.w4a16_gemv
+C1_CASE = ("c1", 4096, 4096, 1)                              # M=1, K=N=4096, G=128
 G = 128
 
 
@@ -170,6 +171,23 @@ def bench_decode(torch, gemm, steps, warmup):
     return {"value": value, "ms_per_step": ms_per_step, "step_bytes": step_bytes,
             "avg_launch_us": avg_launch_us, "bytes_per_launch": step_bytes / len(DECODE_CASES),
             "cases": cases, "copies": copies}
+
+
+def bench_c1(torch, gemm, steps, warmup):
+    """BASELINE configs[0] through w4a16_gemm (M=1, K=N=4096, G=128): the reference's published
+    decode row "o, M=1" (benchmarks/results/latest.json:368-384).  Weights rotate over copies whose
+    working set exceeds twice the Infinity Cache, in one graph; HIP events on the launch stream."""
+    import w4a16_opt
+    name, N, K, M = C1_CASE
+    copies = max(2, -(-2 * MALL_BYTES // (N * K // 2 + (K // G) * N * 2)))
+    w = make_weights(torch, N, K, 105, copies)
+    x = torch.randn(M, K, device="cuda").half()
+    g = graph_of(torch, [lambda Wp=Wp, s=s: gemm(Wp, x, s) for Wp, s in w])
+    reps = [time_graph(torch, [g], max(1, steps // 10), 1) / (max(1, steps // 10) * copies) for _ in range(5)]
+    us = statistics.median(reps) * 1e3
+    gbs = alg_bytes(M, N, K) / (us * 1e-6) / 1e9
+    log(f"decode c1 M={M} N={N} K={K}: {us:.2f} us  {gbs:.0f} GB/s")
+    return {"us": us, "GBs": gbs, "copies": copies, "kernel": w4a16_opt.plan_info(M, N, K, G)["kernel_name"]}
 
 
 def bench_prefill(torch, gemm, steps, warmup):
@@ -324,56 +342,135 @@ def cpu_baseline_quantize(max_seconds=12.0):
             "sample": f"oracle numpy quantize_w4 + pack_int4 on {done} slices of 1024 x {K} fp16 ({dt:.2f} s)"}
 
 
-def cpu_baseline(cases, max_seconds=20.0):
-    """Time the oracle's C restatement of the reference CPU path on the host (bounded sample)."""
-    import numpy as np
-    from oracle import c_oracle, quant
-    nthreads = max(1, min(16, os.cpu_count() or 1))
-    total_b, total_t, done = 0, 0.0, []
-    t_start = time.perf_counter()
-    for name, N, K, M in cases:
-        q, scales = quant.gen_codes_scales(N, K, G, 7)
-        Wp = quant.pack_int4(q)
-        x = np.random.default_rng(8).standard_normal((M, K)).astype(np.float16)
-        c_oracle.forward(Wp, x, scales, N, K, G, nthreads)          # warm-up
+def cpu_threads():
+    """Threads for the CPU baseline: the host's CPUs available to this process, capped by
+    OMP_NUM_THREADS when that is set (the GPU box gives each GPU job a share of its cores)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _median_s(fn, reps):
+    fn()                                                     # warm-up
+    ts = []
+    for _ in range(reps):
         t0 = time.perf_counter()
-        c_oracle.forward(Wp, x, scales, N, K, G, nthreads)
-        dt = time.perf_counter() - t0
-        total_b += alg_bytes(M, N, K)
-        total_t += dt
-        done.append(f"{name} M={M}")
-        if time.perf_counter() - t_start > max_seconds:
-            break
-    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-            "sample": f"oracle C path (unpack + fp16 dequant + fp32 GEMM), one timed call each of: {', '.join(done)}; "
-                      f"{total_t:.2f} s timed, {nthreads} OpenMP threads, host {os.cpu_count()} cpus"}
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
 
 
-def cpu_baseline_prefill(max_seconds=15.0):
-    """Prefill CPU reference rate on a bounded N-slice of config 4 (rate is size-independent)."""
+def _cpu_path_times(torch, N, K, Ms, G, seed, reps):
+    """Median seconds of the reference CPU path (oracle/torch_ref.py: unpack + fp16 dequant, then
+    the fp32 matmul and the fp16 cast) on torch-CPU: (dequant_s, {M: matmul_s})."""
     import numpy as np
-    from oracle import c_oracle, quant
-    nthreads = max(1, min(16, os.cpu_count() or 1))
-    _, N, K, M = PREFILL_CASE
-    Ns = 1024
-    q, scales = quant.gen_codes_scales(Ns, K, G, 9)
-    Wp = quant.pack_int4(q)
-    x = np.random.default_rng(10).standard_normal((M, K)).astype(np.float16)
+    from oracle import quant, torch_ref
+    q, scales = quant.gen_codes_scales(N, K, G, seed)
+    Wp = torch.from_numpy(quant.pack_int4(q))
+    s = torch.from_numpy(scales)
+    del q
+    box = {}
+
+    def dequant():
+        box["W"] = torch_ref.dequantize_w4(torch, torch_ref.unpack_int4(torch, Wp, N, K), s, G)
+    t_deq = _median_s(dequant, reps)
+    W = box.pop("W")
+    t_mm = {}
+    for M in Ms:
+        x = torch.from_numpy(np.random.default_rng([seed, M]).standard_normal((M, K)).astype(np.float16))
+        t_mm[M] = _median_s(lambda: torch_ref.ref_gemm(torch, x, W).half(), reps)
+    return t_deq, t_mm
+
+
+def cpu_baseline(cases, reps=5):
+    """The reference CPU path (unpack, fp16 dequant, fp32 matmul: tests/quant.py:51-59, 77-85)
+    timed on torch-CPU on the host, per decode case: one call = dequant + matmul."""
+    import torch
+    nthreads = cpu_threads()
+    torch.set_num_threads(nthreads)
+    shapes = {}
+    for name, N, K, M in cases:
+        shapes.setdefault((name, N, K), []).append(M)
+    total_b, t_deq_all, t_mm_all, per = 0, 0.0, 0.0, []
     t0 = time.perf_counter()
-    c_oracle.forward(Wp, x, scales, Ns, K, G, nthreads)
-    dt = time.perf_counter() - t0
-    return {"value": round(alg_flops(M, Ns, K) / dt / 1e12, 4), "unit": "TFLOP/s", "cores": nthreads,
-            "kind": "port", "sample": f"oracle C path on an N={Ns} column slice of M=2048, K=8192 ({dt:.2f} s)"}
+    for i, ((name, N, K), Ms) in enumerate(shapes.items()):
+        t_deq, t_mm = _cpu_path_times(torch, N, K, Ms, G, 7 + i, reps)
+        for M in Ms:
+            total_b += alg_bytes(M, N, K)
+            t_deq_all += t_deq
+            t_mm_all += t_mm[M]
+            per.append(f"{name} M={M}: {1e3 * (t_deq + t_mm[M]):.1f} ms")
+    wall = time.perf_counter() - t0
+    tot = t_deq_all + t_mm_all
+    return {"value": round(total_b / tot / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "dequant_s": round(t_deq_all, 4), "matmul_s": round(t_mm_all, 4), "total_s": round(tot, 4),
+            "cpu": cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "sample": f"reference CPU path on torch-CPU (oracle/torch_ref.py: unpack + fp16 (q-8)*s, then "
+                      f"x.float() @ W.float().t() and fp16 cast), each of the {len(cases)} decode calls once "
+                      f"(median of {reps} reps after a warm-up; dequant timed once per weight shape and charged "
+                      f"to every call of that shape): " + "; ".join(per) + f"; {wall:.1f} s wall"}
 
 
-def load_traffic(kind):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary (profiles/), or None."""
+def cpu_baseline_prefill(ns=4096, reps=2):
+    """The reference CPU path on torch-CPU for configs[3] (M=2048, K=8192) on an N-column slice of
+    the weight (the rate does not depend on N): dequant + matmul, median of reps."""
+    import torch
+    nthreads = cpu_threads()
+    torch.set_num_threads(nthreads)
+    _, N, K, M = PREFILL_CASE
+    t0 = time.perf_counter()
+    t_deq, t_mm = _cpu_path_times(torch, ns, K, [M], G, 9, reps)
+    tot = t_deq + t_mm[M]
+    return {"value": round(alg_flops(M, ns, K) / tot / 1e12, 4), "unit": "TFLOP/s", "cores": nthreads,
+            "kind": "port", "dequant_s": round(t_deq, 4), "matmul_s": round(t_mm[M], 4), "total_s": round(tot, 4),
+            "cpu": cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "sample": f"reference CPU path on torch-CPU (oracle/torch_ref.py) for M={M}, K={K} on an N={ns} "
+                      f"column slice of the N={N} weight, median of {reps} reps after a warm-up "
+                      f"({time.perf_counter() - t0:.1f} s wall)"}
+
+
+def load_counters(kind, kernels):
+    """Counter-derived figures for one workload from the committed rocprofv3 PMC summary
+    (profiles/traffic.json): {field: value, "source": ..., "measured_on": [...]}, or None when that
+    file has no entry or its entry was measured on other kernels than `kernels` (the ones this run
+    launched) -- such figures would describe other code."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(kind)
+            ent = json.load(f).get(kind)
     except (OSError, ValueError):
         return None
+    if not isinstance(ent, dict) or sorted(ent.get("kernels", [])) != sorted(set(kernels)):
+        return None
+    return ent
+
+
+def tag_counters(roof, kind, kernels, fields):
+    """Set roof[f] for f in fields from load_counters (None when not measured on these kernels)
+    and name the source of the figures."""
+    ent = load_counters(kind, kernels)
+    for f in fields:
+        roof[f] = ent.get(f) if ent else None
+    roof["counters_source"] = (f"{ent['source']} (rocprofv3 --pmc, measured on the kernels named in kernel)"
+                               if ent else "not measured on these kernels (profiles/traffic.json)")
 
 
 def main(argv=None) -> int:
@@ -416,8 +513,9 @@ def main(argv=None) -> int:
                "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
                "config": {"workload": f"quantize_pack of an fp16 [{N}, {K}] weight (BASELINE configs[3] weight), G={G}"},
                "roofline": {"bound": "hbm", "achieved": round(qr["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(qr["GBs"] / HBM_PEAK_GBS, 4), "traffic": load_traffic("quantize"),
-                            "kernel": "quantize_pack_kernel<_Float16, 128>", "bytes_per_launch": quant_bytes(N, K)}}
+                            "frac": round(qr["GBs"] / HBM_PEAK_GBS, 4),
+                            "kernel": "w4a16::quantize_pack_kernel<_Float16, 128>", "bytes_per_launch": quant_bytes(N, K)}}
+        tag_counters(out["roofline"], "quantize", [out["roofline"]["kernel"]], ["traffic"])
         if not a.no_cpu:
             out["cpu_baseline"] = cpu_baseline_quantize()
         line = json.dumps(out)
@@ -436,11 +534,12 @@ def main(argv=None) -> int:
                                       ", ".join(f"{n} N={N} K={K}" for n, N, K in GEMV_CASES),
                           "timing": "HIP graph replay over rotating weight copies, HIP events"},
                "roofline": {"bound": "hbm", "achieved": round(gv["value"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(gv["value"] / HBM_PEAK_GBS, 4), "traffic": load_traffic("gemv"),
+                            "frac": round(gv["value"] / HBM_PEAK_GBS, 4),
                             "kernel": " + ".join(sorted({c["kernel"] for c in gv["cases"]})),
                             "bytes_per_launch": gv["bytes_per_launch"],
                             "avg_launch_us": round(gv["avg_launch_us"], 3)},
                "cases": gv["cases"]}
+        tag_counters(out["roofline"], "gemv", [c["kernel"] for c in gv["cases"]], ["traffic"])
         if not a.no_cpu:
             out["cpu_baseline"] = cpu_baseline_gemv()
         line = json.dumps(out)
@@ -455,6 +554,7 @@ def main(argv=None) -> int:
         pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
                             a.warmup if a.workload == "prefill" else 3)
     mod = bench_moderate(torch, gemm, 30, 3) if (dec is not None and not a.no_prefill) else None
+    c1 = bench_c1(torch, gemm, 40, 3) if dec is not None else None
     gv = bench_gemv(torch, 20, 3) if (dec is not None and not a.no_prefill) else None
 
     out = {"metric": "decode GB/s & %HBM peak (M=1..16); prefill TFLOP/s & %MFMA peak (M=2048)"}
@@ -468,24 +568,23 @@ def main(argv=None) -> int:
                                    "K=14336 N=4096, M in {1,4,8,16}, G=128; one step = the 8 calls",
                        "G": G, "weight_copies_per_shape": dec["copies"], "timing": f"HIP graph replay ({GRAPH_STEPS} steps per graph), HIP events"},
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": load_traffic("decode"),
+                         "frac": round(ach / HBM_PEAK_GBS, 4),
                          "kernel": " + ".join(sorted({c["kernel"] for c in dec["cases"]})),
                          "bytes_per_launch": dec["bytes_per_launch"],
                          "avg_launch_us": round(dec["avg_launch_us"], 3)},
             "cases": dec["cases"],
         })
+        tag_counters(out["roofline"], "decode", [c["kernel"] for c in dec["cases"]], ["traffic"])
     if pre is not None:
         _, N, K, M = PREFILL_CASE
         pre_obj = {"value": round(pre["TFLOPs"], 1), "unit": "TFLOP/s", "us_per_call": round(pre["us"], 1),
                    "config": {"workload": "BASELINE configs[3]: prefill M=2048 K=8192 N=28672 G=128"},
                    "roofline": {"bound": "mfma", "achieved": round(pre["TFLOPs"], 1), "peak": FP16_MFMA_PEAK_TFS,
                                 "unit": "TFLOP/s", "frac": round(pre["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
-                                "traffic": load_traffic("prefill"), "kernel": pre["kernel"],
-                                "flops_per_launch": alg_flops(M, N, K),
-                                # rocprofv3 counters of the same kernel (profiles/):
-                                # SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)
-                                "mfma_busy_frac": load_traffic("prefill_mfma_util"),
-                                "clock_ghz": load_traffic("prefill_clock_ghz")}}
+                                "kernel": pre["kernel"], "flops_per_launch": alg_flops(M, N, K)}}
+        # rocprofv3 counters of the same kernel: HBM traffic, and the MFMA-busy fraction
+        # SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs) at the measured clock
+        tag_counters(pre_obj["roofline"], "prefill", [pre["kernel"]], ["traffic", "mfma_busy_frac", "clock_ghz"])
         if dec is None:
             out.update({"value": pre_obj["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps,
                         "warmup": a.warmup, "ms_per_step": round(pre["us"] / 1e3, 5), "higher_is_better": True,
@@ -504,6 +603,17 @@ def main(argv=None) -> int:
                          "frac_mfma": round(mod["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
                          "frac_hbm": round(mod["GBs"] / HBM_PEAK_GBS, 4),
                          "flops_per_launch": alg_flops(M, N, K), "bytes_per_launch": alg_bytes(M, N, K, Gm)}}
+    if c1 is not None:
+        _, N, K, M = C1_CASE
+        out["decode_c1"] = {
+            "value": round(c1["GBs"], 1), "unit": "GB/s", "us_per_call": round(c1["us"], 3),
+            "config": {"workload": "BASELINE configs[0]: w4a16_gemm decode M=1 K=4096 N=4096 G=128",
+                       "weight_copies": c1["copies"],
+                       "reference_published": "58.94 us median on an RTX 3050 Laptop GPU "
+                                              "(benchmarks/results/latest.json:368-384)"},
+            "roofline": {"bound": "hbm", "achieved": round(c1["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(c1["GBs"] / HBM_PEAK_GBS, 4), "kernel": c1["kernel"],
+                         "bytes_per_launch": alg_bytes(M, N, K)}}
     if gv is not None:
         out["baseline_gemv"] = {"value": round(gv["value"], 1), "unit": "GB/s",
                                 "frac_hbm": round(gv["value"] / HBM_PEAK_GBS, 4),

@@ -167,7 +167,7 @@ def _kernels(text):
 
 def test_untracked_load_registers_untouched_until_waited(isa):
     ks = _kernels(isa)
-    lds = [k for k in ks if any(n in k for n in ("decode_lds_kernel", "decode_stream_kernel", "decode_ring_kernel",
+    lds = [k for k in ks if any(n in k for n in ("decode_stream_kernel", "decode_ring_kernel",
                                                   "prefill_wide_kernel", "prefill_stream_kernel",
                                                   "prefill_group_kernel"))]
     assert len(lds) >= 16 + 20 + 3 + 2 + 2, list(ks)

@@ -72,8 +72,6 @@ constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m 
 // waves splitting its K range.
 //   kind 0: decode_kernel         weights streamed into VGPRs, pipeline depth d chunks, any
 //                                  chunk count per wave;
-//   kind 1: decode_lds_kernel     weights by direct-to-LDS loads, all d chunks of a wave at once
-//                                  (exactly d chunks per wave);
 //   kind 2: decode_stream_kernel  per-wave ring of d chunk pairs in LDS (the pairs per wave must
 //                                  be a multiple of d);
 //   kind 3: decode_ring_kernel    ring of d + 1 chunk-pair slots (weights, x rows and the pair's
@@ -82,19 +80,17 @@ constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m 
 struct DecodeCfg {
     int kind, nbw, waves, d;
 };
-constexpr DecodeCfg kDecodeTable[40] = {
+constexpr DecodeCfg kDecodeTable[32] = {
     {0, 1, 16, 4}, {0, 1, 16, 2}, {0, 2, 16, 4}, {0, 2, 16, 2},     // 0-3
     {0, 1, 8, 4},  {0, 2, 8, 4},  {0, 4, 8, 4},  {0, 4, 16, 2},     // 4-7
-    {1, 4, 16, 4}, {1, 4, 8, 8},  {1, 4, 8, 7},  {1, 2, 16, 7},     // 8-11
-    {1, 1, 16, 4}, {1, 2, 16, 4}, {1, 2, 8, 4},  {1, 1, 8, 8},      // 12-15
-    {2, 4, 4, 4},  {2, 4, 8, 4},  {2, 2, 4, 4},  {2, 1, 4, 4},      // 16-19
-    {2, 4, 4, 2},  {2, 2, 8, 4},  {2, 1, 8, 4},  {2, 4, 8, 2},      // 20-23
-    {3, 4, 4, 2},  {3, 4, 4, 3},  {3, 4, 8, 1},  {3, 1, 8, 2},      // 24-27
-    {3, 2, 4, 2},  {3, 1, 4, 4},  {3, 2, 8, 1},  {3, 4, 4, 4},      // 28-31
-    {3, 1, 16, 2}, {3, 1, 8, 4},  {3, 2, 8, 2},  {3, 1, 16, 4},     // 32-35
-    {3, 2, 4, 4},  {3, 1, 8, 3},  {3, 2, 16, 2}, {3, 4, 8, 2},      // 36-39
+    {2, 4, 4, 4},  {2, 4, 8, 4},  {2, 2, 4, 4},  {2, 1, 4, 4},      // 8-11
+    {2, 4, 4, 2},  {2, 2, 8, 4},  {2, 1, 8, 4},  {2, 4, 8, 2},      // 12-15
+    {3, 4, 4, 2},  {3, 4, 4, 3},  {3, 4, 8, 1},  {3, 1, 8, 2},      // 16-19
+    {3, 2, 4, 2},  {3, 1, 4, 4},  {3, 2, 8, 1},  {3, 4, 4, 4},      // 20-23
+    {3, 1, 16, 2}, {3, 1, 8, 4},  {3, 2, 8, 2},  {3, 1, 16, 4},     // 24-27
+    {3, 2, 4, 4},  {3, 1, 8, 3},  {3, 2, 16, 2}, {3, 4, 8, 2},      // 28-31
 };
-constexpr int kNumDecodeCfg = 40;
+constexpr int kNumDecodeCfg = 32;
 
 // Token rows per chunk-pair slot of the kind-3 kernel: one row for M = 1 (4-byte x loads in
 // B-operand order), else 4, 8 or 16 rows (16-byte x loads of 4 rows each).
@@ -102,7 +98,6 @@ constexpr int decode_ring_xr(int M) { return M <= 1 ? 1 : M <= 4 ? 4 : M <= 8 ? 
 
 constexpr int decode_lds_bytes(int v, int M) {
     return kDecodeTable[v].kind == 0   ? kDecodeTable[v].waves * kDecodeTable[v].nbw * 64 * 16 + 16
-           : kDecodeTable[v].kind == 1 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * ((kDecodeTable[v].d + 1) / 2) * 1024 + 16
            : kDecodeTable[v].kind == 2 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * kDecodeTable[v].d * 1024 + 16
                                        : kDecodeTable[v].waves * (kDecodeTable[v].d + 1) *
                                              (kDecodeTable[v].nbw * 1088 + decode_ring_xr(M) * 256) + 16;
@@ -111,7 +106,6 @@ constexpr int decode_lds_bytes(int v, int M) {
 // per column tile.
 constexpr bool decode_shape_fits(int v, int KC, int splits, int G) {
     return splits >= 1 && KC % (splits * kDecodeTable[v].waves) == 0 &&
-           (kDecodeTable[v].kind != 1 || KC == splits * kDecodeTable[v].waves * kDecodeTable[v].d) &&
            (kDecodeTable[v].kind != 2 || ((KC / (splits * kDecodeTable[v].waves)) % (2 * kDecodeTable[v].d) == 0)) &&
            (kDecodeTable[v].kind != 3 ||
             ((KC / (splits * kDecodeTable[v].waves)) % 2 == 0 &&

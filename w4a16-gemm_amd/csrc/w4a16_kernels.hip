@@ -82,8 +82,12 @@ __device__ __forceinline__ void decode_finish(f4 sum, bool have, int rb, int lan
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    // Wrapping increment (old >= splits - 1 ? 0 : old + 1): the last arrival sees splits - 1 and
+    // the same instruction returns the counter to zero, so every launch leaves it zero without a
+    // separate reset store.
     if (tid == 0)
-        s_last = __hip_atomic_fetch_add(&counters[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+        s_last = __builtin_amdgcn_atomic_inc32(reinterpret_cast<unsigned*>(&counters[tile]), (unsigned)(splits - 1),
+                                               __ATOMIC_RELAXED, "agent") == (unsigned)(splits - 1);
     __syncthreads();
     if (!s_last) return;
 
@@ -115,7 +119,6 @@ __device__ __forceinline__ void decode_finish(f4 sum, bool have, int rb, int lan
         }
         *reinterpret_cast<u2*>(y + (size_t)m * N + nn) = pack_f16x4(tot);
     }
-    if (tid == 0) __hip_atomic_store(&counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int NBW, int WAVES, int D>
@@ -195,124 +198,6 @@ decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         sum = red[0][rb][lane];
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) sum += red[w][rb][lane];
-    }
-    decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
-}
-
-
-// Decode with the weights streamed by direct-to-LDS loads (global_load_lds_dwordx4): a wave
-// issues every weight chunk of its K range at once without holding them in VGPRs, and without
-// the duplicated 16-byte requests of the register path (lanes i and i+8 read the same word quad
-// back from LDS instead).  Chunks 2p and 2p+1 of one n16 block are 1 KB contiguous in Wp and
-// land contiguously in LDS from one instruction.  The compiler does not order a ds_read after
-// the LDS-DMA that fills it, so the kernel (a) pins the issue order with compiler barriers --
-// x fragments and scales first, then the DMAs pair by pair -- and (b) waits with an explicit
-// s_waitcnt vmcnt(#DMAs issued after pair p) before reading pair p.  Same tiling, reduction
-// and split-K hand-off as decode_kernel; KCW (chunks per wave) is a compile-time constant.
-
-template <int NBW, int WAVES, int KCW>
-__global__ void __launch_bounds__(WAVES * 64)
-decode_lds_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
-                  const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                  float* __restrict__ ws, int* __restrict__ counters,
-                  int M, int N, int K, int gshift, int splits) {
-    constexpr int NPAIR = (KCW + 1) / 2;
-    constexpr int WAVE_BYTES = NBW * NPAIR * 1024;          // [n16 block][chunk pair][1 KB]
-    static_assert(NPAIR >= 1 && (NPAIR - 1) * NBW <= 63, "too many DMAs in flight for vmcnt");
-    __shared__ __attribute__((aligned(16))) char wl[WAVES * WAVE_BYTES];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int kb = lane >> 4;
-    const int li = lane & 15;
-    const int split = blockIdx.x % splits;
-    const int tile = blockIdx.x / splits;
-    const int KC = K >> 6;
-    const int kc0 = (split * WAVES + wave) * KCW;
-    const int nb0 = tile * NBW;
-    const int lanep = ((li & 7) << 2) | kb;
-    char* wreg = wl + wave * WAVE_BYTES;
-
-    // 1. x fragments and scales of all KCW chunks, issued through asm so that the compiler does
-    //    not wait for them (it would wait with vmcnt(0), i.e. for every DMA as well).
-    const uint16_t* xsrc = x + (size_t)min(li, M - 1) * K + (size_t)kc0 * 64 + kb * 8;
-    u4 xq[KCW][2];
-#pragma unroll
-    for (int c = 0; c < KCW; ++c) {
-        xq[c][0] = gload_u4_untracked(xsrc + (size_t)c * 64);
-        xq[c][1] = gload_u4_untracked(xsrc + (size_t)c * 64 + 32);
-    }
-    uint32_t sq[NBW][KCW];
-#pragma unroll
-    for (int b = 0; b < NBW; ++b)
-#pragma unroll
-        for (int c = 0; c < KCW; ++c)
-            sq[b][c] = gload_u16_untracked(scales + (size_t)((kc0 + c) >> gshift) * N + (size_t)(nb0 + b) * 16 + li);
-    asm volatile("" ::: "memory");
-
-    // 2. weight DMAs, pair by pair (lanes 0-31: chunk 2p, lanes 32-63: chunk 2p+1).
-#pragma unroll
-    for (int p = 0; p < NPAIR; ++p)
-#pragma unroll
-        for (int b = 0; b < NBW; ++b) {
-            const u4* src = Wp + ((size_t)(nb0 + b) * KC + kc0 + 2 * p) * 32 + lane;
-            auto* dst = (__attribute__((address_space(3))) void*)(wreg + (b * NPAIR + p) * 1024);
-            if (2 * p + 1 < KCW || lane < 32) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, kWeightStreamPolicy);
-        }
-    asm volatile("" ::: "memory");
-
-    // 3. dequantise + MFMA in K order, waiting for each pair's DMAs.  The LDS reads of DMA'd
-    //    data are issued through asm (lds_read_u4) so that the only waits are the explicit ones.
-    const Dq d = dq_setup(lane);
-    const uint32_t wbase_lane = (uint32_t)reinterpret_cast<uintptr_t>(wreg) + lanep * 16;
-    f4 acc[NBW];
-#pragma unroll
-    for (int b = 0; b < NBW; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int p = 0; p < NPAIR; ++p) {
-        wait_vmcnt((NPAIR - 1 - p) * NBW);
-        if (p == 0) {                       // x and scales were issued before every DMA
-#pragma unroll
-            for (int c = 0; c < KCW; ++c) { bind_after_wait(xq[c][0]); bind_after_wait(xq[c][1]); }
-#pragma unroll
-            for (int b = 0; b < NBW; ++b)
-#pragma unroll
-                for (int c = 0; c < KCW; ++c) bind_after_wait(sq[b][c]);
-        }
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int c = 2 * p + cc;
-            if (c >= KCW) break;
-            const h8 b0 = __builtin_bit_cast(h8, xpose_rows(xq[c][0]));
-            const h8 b1 = __builtin_bit_cast(h8, xpose_rows(xq[c][1]));
-            u4 wv[NBW];
-#pragma unroll
-            for (int b = 0; b < NBW; ++b) wv[b] = lds_read_u4(wbase_lane + (b * NPAIR + p) * 1024 + cc * 512);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-            for (int b = 0; b < NBW; ++b) bind_after_wait(wv[b]);
-#pragma unroll
-            for (int b = 0; b < NBW; ++b) {
-                const u4 w = wv[b];
-                const h2 s2 = scale2((uint16_t)sq[b][c]);
-                acc[b] = mfma16x16x32(dq_frag(w.x, w.y, d, s2), b0, acc[b]);
-                acc[b] = mfma16x16x32(dq_frag(w.z, w.w, d, s2), b1, acc[b]);
-            }
-        }
-    }
-
-    // 4. cross-wave reduction in wave order; each wave parks its tile in its own LDS region.
-    f4* red = reinterpret_cast<f4*>(wreg);
-#pragma unroll
-    for (int b = 0; b < NBW; ++b) red[b * 64 + lane] = acc[b];
-    __syncthreads();
-    f4 sum = {0.f, 0.f, 0.f, 0.f};
-    const int rb = tid >> 6;
-    if (tid < NBW * 64) {
-        sum = reinterpret_cast<const f4*>(wl)[rb * 64 + lane];
-#pragma unroll
-        for (int w = 1; w < WAVES; ++w) sum += reinterpret_cast<const f4*>(wl + w * WAVE_BYTES)[rb * 64 + lane];
     }
     decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
 }
@@ -417,16 +302,16 @@ decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     for (int p0 = 0; p0 + D < npair; p0 += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
-            wait_vmcnt((D - 1) * OPS);
+            wait_vmcnt<(D - 1) * OPS>();
             consume(s);
             issue(p0 + D + s, s);
         }
     }
-#pragma unroll
-    for (int s = 0; s < D; ++s) {
-        wait_vmcnt((D - 1 - s) * OPS);
-        consume(s);
-    }
+    static_for<0, D>([&](auto t) {
+        constexpr int T = decltype(t)::value;
+        wait_vmcnt<(D - 1 - T) * OPS>();
+        consume(T);
+    });
 
     // Cross-wave reduction in wave order; each wave parks its tile in its own LDS region.
     f4* red = reinterpret_cast<f4*>(wreg);
@@ -651,7 +536,7 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     for (; p + S <= nsteady; p += S) {
         static_for<0, S>([&](auto t) {
             constexpr int T = decltype(t)::value;
-            wait_vmcnt((D - 1) * OPS);
+            wait_vmcnt<(D - 1) * OPS>();
             issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
             consume(p + T, t);
         });
@@ -660,13 +545,13 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         constexpr int R = decltype(r)::value;
         static_for<0, R>([&](auto t) {
             constexpr int T = decltype(t)::value;
-            wait_vmcnt((D - 1) * OPS);
+            wait_vmcnt<(D - 1) * OPS>();
             issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
             consume(p + T, t);
         });
         static_for<0, D>([&](auto t) {
             constexpr int T = decltype(t)::value;
-            wait_vmcnt((D - 1 - T) * OPS);
+            wait_vmcnt<(D - 1 - T) * OPS>();
             consume(p + R + T, std::integral_constant<int, (R + T) % S>{});
         });
     });
@@ -944,18 +829,17 @@ prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     int sc = 0, si = D;
     int p = 0;
     for (; p + D < npair; ++p) {
-        wait_vmcnt((D - 1) * OPS);
+        wait_vmcnt<(D - 1) * OPS>();
         issue(p + D, si);
         consume(sc);
         sc = sc + 1 == S ? 0 : sc + 1;
         si = si + 1 == S ? 0 : si + 1;
     }
-#pragma unroll
-    for (int t = 0; t < D; ++t) {
-        wait_vmcnt((D - 1 - t) * OPS);
+    static_for<0, D>([&](auto t) {
+        wait_vmcnt<(D - 1 - decltype(t)::value) * OPS>();
         consume(sc);
         sc = sc + 1 == S ? 0 : sc + 1;
-    }
+    });
 
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
@@ -1152,7 +1036,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     for (; p + S <= nsteady; p += S) {
         static_for<0, S>([&](auto t) {
             constexpr int T = decltype(t)::value;
-            wait_vmcnt((D - 1) * OPS);
+            wait_vmcnt<(D - 1) * OPS>();
             __builtin_amdgcn_s_barrier();
             issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
             consume(t);
@@ -1162,14 +1046,14 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         constexpr int R = decltype(r)::value;
         static_for<0, R>([&](auto t) {
             constexpr int T = decltype(t)::value;
-            wait_vmcnt((D - 1) * OPS);
+            wait_vmcnt<(D - 1) * OPS>();
             __builtin_amdgcn_s_barrier();
             issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
             consume(t);
         });
         static_for<0, D>([&](auto t) {
             constexpr int T = decltype(t)::value;
-            wait_vmcnt((D - 1 - T) * OPS);
+            wait_vmcnt<(D - 1 - T) * OPS>();
             __builtin_amdgcn_s_barrier();
             consume(std::integral_constant<int, (R + T) % S>{});
         });
@@ -1267,8 +1151,7 @@ static hipError_t launch_decode_v(const w4a16_plan& p, const u4* Wp, const uint1
         }
 #undef W4A16_RING
     } else {
-        hipLaunchKernelGGL((decode_lds_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
-                           Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits);
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -1285,8 +1168,6 @@ static hipError_t launch_decode(const w4a16_plan& p, const u4* Wp, const uint16_
         W4A16_DEC_CASE(20) W4A16_DEC_CASE(21) W4A16_DEC_CASE(22) W4A16_DEC_CASE(23)
         W4A16_DEC_CASE(24) W4A16_DEC_CASE(25) W4A16_DEC_CASE(26) W4A16_DEC_CASE(27)
         W4A16_DEC_CASE(28) W4A16_DEC_CASE(29) W4A16_DEC_CASE(30) W4A16_DEC_CASE(31)
-        W4A16_DEC_CASE(32) W4A16_DEC_CASE(33) W4A16_DEC_CASE(34) W4A16_DEC_CASE(35)
-        W4A16_DEC_CASE(36) W4A16_DEC_CASE(37) W4A16_DEC_CASE(38) W4A16_DEC_CASE(39)
 #undef W4A16_DEC_CASE
         default: return hipErrorInvalidValue;
     }

@@ -207,16 +207,16 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             };
             auto ntiles_of = [&](int cand) { return N / (16 * kDecodeTable[cand].nbw); };
             struct Cand { int v, sp; };
-            Cand wide_small_m[] = {{28, 1}, {20, 1}, {7, 1}};
-            Cand wide[] = {{24, 1}, {20, 1}, {7, 1}};
-            Cand longk_m4[] = {{37, 1}, {27, 1}, {30, 2}};
-            Cand longk_small_m[] = {{27, 1}, {30, 2}, {30, 2}};
-            Cand longk_large_m[] = {{28, 2}, {30, 2}, {27, 1}};
-            Cand shortk_m1[] = {{37, 1}, {27, 1}, {22, 1}};
-            Cand shortk[] = {{27, 1}, {29, 1}, {29, 1}};
+            Cand wide_small_m[] = {{20, 1}, {12, 1}, {7, 1}};
+            Cand wide[] = {{16, 1}, {12, 1}, {7, 1}};
+            Cand longk_m4[] = {{29, 1}, {19, 1}, {22, 2}};
+            Cand longk_small_m[] = {{19, 1}, {22, 2}, {22, 2}};
+            Cand longk_large_m[] = {{20, 2}, {22, 2}, {19, 1}};
+            Cand shortk_m1[] = {{29, 1}, {19, 1}, {14, 1}};
+            Cand shortk[] = {{19, 1}, {21, 1}, {21, 1}};
             Cand* list;
             const int n = 3;
-            if ((int64_t)ntiles_of(20) * 8 >= 7LL * cus) list = M <= 4 ? wide_small_m : wide;
+            if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus) list = M <= 4 ? wide_small_m : wide;
             else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
             else list = M <= 1 ? shortk_m1 : shortk;
             for (int i = 0; i < n && var < 0; ++i)

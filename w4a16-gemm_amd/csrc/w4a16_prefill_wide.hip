@@ -228,17 +228,17 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     load_w(1, w1, s1);
     __syncthreads();
     for (int kc = 0; kc < KC; kc += 2) {
-        wait_vmcnt(WAIT_X);
+        wait_vmcnt<WAIT_X>();
         store_x(1, xr1);
         load_x(kc + 3, xr1);
-        wait_vmcnt(WAIT_W);
+        wait_vmcnt<WAIT_W>();
         compute(0, w0, s0);
         load_w(kc + 2, w0, s0);
         __syncthreads();
-        wait_vmcnt(WAIT_X);
+        wait_vmcnt<WAIT_X>();
         store_x(0, xr0);
         load_x(kc + 4, xr0);
-        wait_vmcnt(WAIT_W);
+        wait_vmcnt<WAIT_W>();
         compute(1, w1, s1);
         load_w(kc + 3, w1, s1);
         __syncthreads();

@@ -24,28 +24,26 @@
 
 namespace {
 
-// Per-device decode split-K counters.  Zeroed once when created; every decode launch leaves
-// them zero again (w4a16.h).  Creating them allocates and fills, so the first decode call on
-// a device must not be inside HIP graph capture (the reference likewise expects one eager
-// call before capture: tests/test_w4a16.py:269).
+// Decode split-K counters.  Launches that share a counter buffer must not overlap in time
+// (w4a16.h), and work on different streams may overlap, so eager calls keep one buffer per
+// (device, stream): zeroed when created, left zero by every launch.  Under HIP graph capture the
+// buffer is allocated per call from the capture's memory pool and zeroed by a fill kernel that
+// the graph records, so every replay starts from zero counters and no buffer is shared between a
+// graph and eager work.  The returned tensor must stay alive until the launch is enqueued.
 std::mutex g_mu;
-std::map<int, at::Tensor> g_counters;
+std::map<std::pair<int, hipStream_t>, at::Tensor> g_counters;
 
-int32_t* decode_counters(const at::Tensor& like, hipStream_t stream) {
-    const int dev = like.device().index();
+at::Tensor decode_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    TORCH_CHECK(hipStreamIsCapturing(stream, &st) == hipSuccess, "hipStreamIsCapturing failed");
+    const auto opts = like.options().dtype(torch::kInt32);
+    if (st != hipStreamCaptureStatusNone) return torch::zeros({(int64_t)slots}, opts);
+    const std::pair<int, hipStream_t> key{(int)like.device().index(), stream};
     std::lock_guard<std::mutex> lk(g_mu);
-    auto it = g_counters.find(dev);
-    if (it == g_counters.end()) {
-        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-        TORCH_CHECK(hipStreamIsCapturing(stream, &st) == hipSuccess, "hipStreamIsCapturing failed");
-        TORCH_CHECK(st == hipStreamCaptureStatusNone,
-                    "w4a16_gemm: the first decode call on a device must run outside graph capture "
-                    "(it creates the split-K counter buffer); call it once eagerly before capturing");
-        at::Tensor t = torch::zeros({(int64_t)w4a16_max_counter_slots()},
-                                    like.options().dtype(torch::kInt32));
-        it = g_counters.emplace(dev, t).first;
-    }
-    return it->second.data_ptr<int32_t>();
+    auto it = g_counters.find(key);
+    if (it == g_counters.end())
+        it = g_counters.emplace(key, torch::zeros({(int64_t)w4a16_max_counter_slots()}, opts)).first;
+    return it->second;
 }
 
 w4a16_device_limits limits_for(int dev) {
@@ -96,7 +94,12 @@ torch::Tensor w4a16_gemm(torch::Tensor Wp, torch::Tensor x, torch::Tensor scales
         ws = torch::empty({(int64_t)plan.workspace_bytes}, x.options().dtype(torch::kUInt8));
         ws_ptr = ws.data_ptr();
     }
-    int32_t* cnt = plan.counter_slots ? decode_counters(x, stream) : nullptr;
+    torch::Tensor cnt_t;
+    int32_t* cnt = nullptr;
+    if (plan.counter_slots) {
+        cnt_t = decode_counters(x, stream, plan.counter_slots);
+        cnt = cnt_t.data_ptr<int32_t>();
+    }
 
     const int lrc = w4a16_launch(&plan, static_cast<const int32_t*>(prob.Wp),
                                  static_cast<const uint16_t*>(prob.x), static_cast<const uint16_t*>(prob.scales),
@@ -152,8 +155,7 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
         return s + ">";
     };
     if (plan.kernel == W4A16_VARIANT_DECODE) {
-        static const char* const kinds[] = {"decode_kernel", "decode_lds_kernel", "decode_stream_kernel",
-                                            "decode_ring_kernel"};
+        static const char* const kinds[] = {"decode_kernel", "", "decode_stream_kernel", "decode_ring_kernel"};
         const w4a16::DecodeCfg& c = w4a16::kDecodeTable[plan.decode_variant];
         d["kernel_name"] = c.kind == 3 ? tmpl(kinds[3], {c.nbw, c.waves, c.d, w4a16::decode_ring_xr((int)M)})
                                        : tmpl(kinds[c.kind], {c.nbw, c.waves, c.d});
