@@ -100,6 +100,26 @@ int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
                  const uint16_t* scales, uint16_t* y, void* workspace, int32_t* counters,
                  void* stream);
 
+/* Scratch limits of w4a16_launch_noalloc: fp32 partials and split-K counters it can hold. */
+#define W4A16_NOALLOC_MAX_WORKSPACE_BYTES (4u << 20)
+#define W4A16_NOALLOC_MAX_COUNTER_SLOTS   16384
+
+/* w4a16_launch without a caller-provided workspace: the same kernels, with the split-K partials
+ * and counters in a static device array of the library (4 MiB + 64 KiB per GPU, held until the
+ * process ends).  No counterpart in the reference (its decode path needs no scratch); it is for
+ * callers that cannot allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  It allocates nothing (no hipMalloc, no allocating library
+ * call); the caller passes only the inputs and y.  Runs on the current HIP device, on `stream`.
+ * The first call on a device resolves the array's address and clears its counters with a small
+ * kernel on `stream`.  Every call on one GPU shares that GPU's array: calls whose plans have
+ * workspace_bytes > 0 must not overlap in time on one GPU (they race on the partials and
+ * counters); plans without a workspace (prefill, unsplit decode) use no scratch.
+ * Returns W4A16_OK, W4A16_ERR_WORKSPACE when plan->workspace_bytes exceeds
+ * W4A16_NOALLOC_MAX_WORKSPACE_BYTES or plan->counter_slots exceeds W4A16_NOALLOC_MAX_COUNTER_SLOTS
+ * (message via w4a16_last_error), or W4A16_ERR_HIP. */
+int w4a16_launch_noalloc(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
+                         const uint16_t* scales, uint16_t* y, void* stream);
+
 /* Quantise and pack a weight matrix on the device (asynchronous, no allocation).
  * Replaces the reference's torch-side quantize_w4 + pack_int4 (tests/quant.py:62-74, 34-48),
  * the producer of the Wp and scales that w4a16_gemm consumes:

@@ -1,0 +1,115 @@
+"""GPU test of w4a16_launch_noalloc (include/w4a16.h): the allocation-free launch, called through
+the C ABI, against the existing entry point w4a16_launch on the same plan.
+
+Both are called through ctypes on torch's current stream; w4a16_launch gets a torch workspace and
+a zeroed counter buffer, w4a16_launch_noalloc only the inputs and y.  Two calls in a row, the
+second with a smaller input, must each equal w4a16_launch bit for bit (same kernels, same
+reduction order) and the oracle within the reference tolerance.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import pytest
+
+from tests._helpers import PKG, assert_close, gemm, make_problem, ref_gemm, torch_cuda
+from tests.test_abi_host import Limits, Plan, Problem
+
+pytestmark = pytest.mark.gpu
+
+W4A16_ERR_WORKSPACE = 4
+
+
+def _lib():
+    import w4a16_opt  # noqa: F401  (loads libw4a16_hip.so through its rpath; ctypes gets the same copy)
+    L = ctypes.CDLL(os.path.join(PKG, "libw4a16_hip.so"))
+    L.w4a16_plan_create.argtypes = [ctypes.POINTER(Problem), ctypes.c_int, ctypes.POINTER(Limits),
+                                    ctypes.POINTER(Plan), ctypes.c_char_p, ctypes.c_size_t]
+    L.w4a16_query_device.argtypes = [ctypes.c_int, ctypes.POINTER(Limits)]
+    L.w4a16_launch.argtypes = [ctypes.POINTER(Plan)] + [ctypes.c_void_p] * 7
+    L.w4a16_launch_noalloc.argtypes = [ctypes.POINTER(Plan)] + [ctypes.c_void_p] * 5
+    L.w4a16_last_error.restype = ctypes.c_char_p
+    return L
+
+
+def _plan(L, torch, Wp, x, scales, G):
+    M, K = x.shape
+    N = scales.shape[1]
+    lim = Limits()
+    assert L.w4a16_query_device(torch.cuda.current_device(), ctypes.byref(lim)) == 0
+    prob = Problem(M, K, N, K // G, Wp.numel(), Wp.data_ptr(), x.data_ptr(), scales.data_ptr())
+    plan = Plan()
+    err = ctypes.create_string_buffer(512)
+    rc = L.w4a16_plan_create(ctypes.byref(prob), -1, ctypes.byref(lim), ctypes.byref(plan), err, 512)
+    assert rc == 0, err.value
+    return plan
+
+
+def _both(L, torch, Wp, x, scales, G):
+    """(y from w4a16_launch_noalloc, y from w4a16_launch, plan)."""
+    plan = _plan(L, torch, Wp, x, scales, G)
+    st = torch.cuda.current_stream().cuda_stream
+    M, N = x.shape[0], scales.shape[1]
+    y_na = torch.empty(M, N, dtype=torch.half, device="cuda")
+    rc = L.w4a16_launch_noalloc(ctypes.byref(plan), Wp.data_ptr(), x.data_ptr(), scales.data_ptr(),
+                                y_na.data_ptr(), st)
+    assert rc == 0, L.w4a16_last_error()
+    y = torch.empty_like(y_na)
+    ws = torch.empty(max(1, plan.workspace_bytes), dtype=torch.uint8, device="cuda")
+    cnt = torch.zeros(max(1, plan.counter_slots), dtype=torch.int32, device="cuda")
+    rc = L.w4a16_launch(ctypes.byref(plan), Wp.data_ptr(), x.data_ptr(), scales.data_ptr(), y.data_ptr(),
+                        ws.data_ptr(), cnt.data_ptr(), st)
+    assert rc == 0, L.w4a16_last_error()
+    torch.cuda.synchronize()
+    return y_na, y, plan
+
+
+def test_noalloc_matches_launch_two_calls():
+    torch = torch_cuda()
+    L = _lib()
+    G = 128
+    x, q, scales, Wp, key = make_problem(16, 256, 14336, G, seed=51)
+    print("noalloc call 1: M=16 N=256 K=14336", flush=True)
+    y_na, y, plan = _both(L, torch, Wp, x, scales, G)
+    assert plan.kernel == 0 and plan.splits > 1 and plan.workspace_bytes > 0, (plan.splits, plan.workspace_bytes)
+    assert torch.equal(y_na, y)
+    assert_close(y_na, ref_gemm(x, q, scales, G, key))
+    x2 = x[:5].contiguous()
+    print("noalloc call 2: M=5 N=256 K=14336", flush=True)
+    y2_na, y2, plan2 = _both(L, torch, Wp, x2, scales, G)
+    assert plan2.splits > 1 and 0 < plan2.workspace_bytes < plan.workspace_bytes
+    assert torch.equal(y2_na, y2)
+    assert_close(y2_na, ref_gemm(x2, q, scales, G, key))
+    assert torch.equal(y2_na, gemm(Wp, x2, scales))
+
+
+def test_noalloc_prefill_and_unsplit_decode():
+    """Plans without a workspace run through the same entry point unchanged."""
+    torch = torch_cuda()
+    L = _lib()
+    for M, N, K, G in ((40, 512, 2048, 64), (1, 4096, 4096, 128)):
+        print(f"noalloc M={M} N={N} K={K} G={G}", flush=True)
+        x, q, scales, Wp, key = make_problem(M, N, K, G, seed=52)
+        y_na, y, plan = _both(L, torch, Wp, x, scales, G)
+        assert plan.workspace_bytes == 0
+        assert torch.equal(y_na, y)
+        assert_close(y_na, ref_gemm(x, q, scales, G, key))
+
+
+def test_noalloc_rejects_plans_beyond_the_scratch(monkeypatch):
+    """A plan whose partials exceed the static scratch is refused before any launch."""
+    torch = torch_cuda()
+    L = _lib()
+    monkeypatch.setenv("W4A16_DECODE", "4,4")           # register decode kernel, 4 K splits
+    M, N, K, G = 16, 32768, 4096, 128
+    lim = Limits()
+    assert L.w4a16_query_device(torch.cuda.current_device(), ctypes.byref(lim)) == 0
+    prob = Problem(M, K, N, K // G, N * K // 8, 0, 0, 0)
+    plan = Plan()
+    err = ctypes.create_string_buffer(512)
+    assert L.w4a16_plan_create(ctypes.byref(prob), -1, ctypes.byref(lim), ctypes.byref(plan), err, 512) == 0
+    assert plan.splits == 4 and plan.workspace_bytes == 4 * M * N * 4 > 4 << 20
+    rc = L.w4a16_launch_noalloc(ctypes.byref(plan), 0, 0, 0, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == W4A16_ERR_WORKSPACE
+    assert b"static scratch" in L.w4a16_last_error()

@@ -9,6 +9,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "w4a16.h"
 #include "w4a16_asm.h"
@@ -1176,6 +1177,80 @@ static hipError_t launch_decode(const w4a16_plan& p, const u4* Wp, const uint16_
 }  // namespace w4a16
 
 using namespace w4a16;
+
+// ------------------------------------------------------------------ allocation-free launches
+// Scratch of w4a16_launch_noalloc: the split-K counters (first W4A16_NOALLOC_MAX_COUNTER_SLOTS
+// ints) followed by the fp32 partials (W4A16_NOALLOC_MAX_WORKSPACE_BYTES).  Each device holds its
+// own copy for the life of the process.  The counters start at zero (zero-initialised storage,
+// and cleared once more when a device is first used) and every launch leaves them zero (the
+// wrapping increment in decode_finish).
+namespace {
+constexpr size_t kScratchCounterBytes = (size_t)W4A16_NOALLOC_MAX_COUNTER_SLOTS * sizeof(int32_t);
+constexpr size_t kScratchBytes = kScratchCounterBytes + (size_t)W4A16_NOALLOC_MAX_WORKSPACE_BYTES;
+static_assert(kScratchCounterBytes % 256 == 0, "partials start 256-byte aligned");
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+__global__ void __launch_bounds__(256) scratch_clear_kernel(u4* __restrict__ p, int n16) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n16) p[i] = u4{0u, 0u, 0u, 0u};
+}
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxScratchDevices];      // device address of `scratch` per device, or null
+
+// The device address of this device's scratch (resolved and cleared on first use), or null with
+// the message set.
+char* scratch_for_current_device(hipStream_t st) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+        w4a16_set_last_error("w4a16_launch_noalloc: no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            w4a16_set_last_error(e != hipSuccess ? hipGetErrorString(e) : "hipGetSymbolAddress returned null");
+            return nullptr;
+        }
+        constexpr int n16 = (int)(kScratchCounterBytes / 16);
+        hipLaunchKernelGGL(scratch_clear_kernel, dim3((n16 + 255) / 256), dim3(256), 0, st,
+                           static_cast<u4*>(ptr), n16);
+        const hipError_t le = hipGetLastError();
+        if (le != hipSuccess) {
+            w4a16_set_last_error(hipGetErrorString(le));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = static_cast<char*>(ptr);
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int w4a16_launch_noalloc(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
+                                    const uint16_t* scales, uint16_t* y, void* stream) {
+    if (!plan) return W4A16_ERR_INVALID;
+    if (plan->workspace_bytes > (uint64_t)W4A16_NOALLOC_MAX_WORKSPACE_BYTES ||
+        plan->counter_slots > W4A16_NOALLOC_MAX_COUNTER_SLOTS) {
+        char msg[256];
+        std::snprintf(msg, sizeof(msg),
+                      "w4a16_launch_noalloc: the plan needs %llu bytes of partials and %d counters; the static "
+                      "scratch holds %llu bytes and %d counters (use w4a16_launch with a workspace)",
+                      (unsigned long long)plan->workspace_bytes, plan->counter_slots,
+                      (unsigned long long)W4A16_NOALLOC_MAX_WORKSPACE_BYTES, W4A16_NOALLOC_MAX_COUNTER_SLOTS);
+        w4a16_set_last_error(msg);
+        return W4A16_ERR_WORKSPACE;
+    }
+    char* base = nullptr;
+    if (plan->workspace_bytes || plan->counter_slots) {
+        base = scratch_for_current_device(reinterpret_cast<hipStream_t>(stream));
+        if (!base) return W4A16_ERR_HIP;
+    }
+    return w4a16_launch(plan, Wp, x, scales, y, base ? base + kScratchCounterBytes : nullptr,
+                        base ? reinterpret_cast<int32_t*>(base) : nullptr, stream);
+}
 
 extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
                             const uint16_t* scales, uint16_t* y, void* workspace, int32_t* counters,
