@@ -479,10 +479,11 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=20)
-    ap.add_argument("--workload", choices=("decode", "prefill", "quantize", "gemv", "copy"), default="decode",
-                    help="quantize: device quantise+pack of the prefill weight; gemv: the baseline GEMV "
-                         "(w4a16_ext); copy: HBM-counter calibration kernel (64 MiB elementwise copy), no "
-                         "benchmark line")
+    ap.add_argument("--workload", choices=("decode", "prefill", "moderate", "quantize", "gemv", "copy"),
+                    default="decode",
+                    help="prefill: configs[3] alone; moderate: configs[2] alone; quantize: device quantise+pack of "
+                         "the prefill weight; gemv: the baseline GEMV (w4a16_ext); copy: HBM-counter calibration "
+                         "kernel (64 MiB elementwise copy), no benchmark line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--json", default=None, help="also write the JSON line to this file")
@@ -542,6 +543,25 @@ def main(argv=None) -> int:
         tag_counters(out["roofline"], "gemv", [c["kernel"] for c in gv["cases"]], ["traffic"])
         if not a.no_cpu:
             out["cpu_baseline"] = cpu_baseline_gemv()
+        line = json.dumps(out)
+        print(line, flush=True)
+        if a.json:
+            with open(a.json, "w") as f:
+                f.write(line + "\n")
+        return 0
+    if a.workload == "moderate":
+        mod = bench_moderate(torch, gemm, a.steps, a.warmup)
+        _, N, K, M, Gm = MODERATE_CASE
+        out = {"metric": "prefill TFLOP/s & %MFMA peak at moderate batch (BASELINE configs[2])",
+               "value": round(mod["TFLOPs"], 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+               "ms_per_step": round(mod["us"] * mod["copies"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+               "vs_baseline": None, "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
+               "config": {"workload": f"BASELINE configs[2]: prefill M={M} K={K} N={N} G={Gm}; one step = one call "
+                                      f"on each of {mod['copies']} weight copies"},
+               "roofline": {"bound": "mfma", "achieved": round(mod["TFLOPs"], 1), "peak": FP16_MFMA_PEAK_TFS,
+                            "unit": "TFLOP/s", "frac": round(mod["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
+                            "frac_hbm": round(mod["GBs"] / HBM_PEAK_GBS, 4), "kernel": mod["kernel"],
+                            "flops_per_launch": alg_flops(M, N, K), "bytes_per_launch": alg_bytes(M, N, K, Gm)}}
         line = json.dumps(out)
         print(line, flush=True)
         if a.json:

@@ -3,7 +3,8 @@
     python tests/golden/make_golden.py
 
 It is a regression fixture of the oracle (oracle/quant.py), which is itself pinned by
-tests/test_oracle.py; the GPU tests also use it as a fixed bit-level target.  The reference
+tests/test_oracle.py (test_golden_small_problem_regression re-derives every array bit for bit);
+the GPU tests run the op on its inputs against its y_ref (test_golden_small_problem).  The reference
 ships no vector files and its Python oracle is not executed here (every function is pinned by
 closed forms, hand-derived known answers and exhaustive checks instead).
 """

@@ -30,14 +30,14 @@ def _args(argv):
 
 
 def test_defaults_mirror_the_reference_sweep():
-    a = _args({})
-    assert [n for n, _ in bench_gemm.parse_shapes(a)] == ["qkv", "o", "gate_up", "down"]
-    assert dict(bench_gemm.parse_shapes(a))["gate_up"] == (28672, 4096)
-    assert bench_gemm.parse_phase_m(a) == {"prefill": [128, 512, 1024, 2048, 4096, 8192], "decode": [1, 2, 4, 8, 16, 32]}
-    assert bench_gemm.parse_phase_m(_args({"phase": "decode", "M": "3,3,5"})) == {"decode": [3, 5]}
-    assert bench_gemm.parse_shapes(_args({"shape": ["256,1024"]})) == [("256x1024", (256, 1024))]
+    shapes, phase_m = bench_gemm.sweep_cases(_args({}))
+    assert [n for n, _ in shapes] == ["qkv", "o", "gate_up", "down"]
+    assert dict(shapes)["gate_up"] == (28672, 4096)
+    assert phase_m == {"prefill": [128, 512, 1024, 2048, 4096, 8192], "decode": [1, 2, 4, 8, 16, 32]}
+    assert bench_gemm.sweep_cases(_args({"phase": "decode", "M": "3,3,5"}))[1] == {"decode": [3, 5]}
+    assert bench_gemm.sweep_cases(_args({"shape": ["256,1024"]}))[0] == [("256x1024", (256, 1024))]
     with pytest.raises(ValueError):
-        bench_gemm.parse_phase_m(_args({"M": "0"}))
+        bench_gemm.sweep_cases(_args({"M": "0"}))
 
 
 def test_row_and_document_schema():
@@ -53,12 +53,6 @@ def test_row_and_document_schema():
     assert doc["parameters"]["backends"] == ["HIP W4A16", "hipBLASLt fp16"]
     json.dumps(doc)
     assert "hip us" in bench_gemm.format_table([row], markdown=True)
-
-
-def test_copies_reach_the_working_set():
-    assert bench_gemm.n_copies(30 * 2**20, 1024) == 35
-    assert bench_gemm.n_copies(2**20, 1024) == 64            # capped like the reference
-    assert bench_gemm.n_copies(2**31, 1024) == 1
 
 
 @pytest.mark.parametrize("N,K,G", [(32, 128, 64), (48, 256, 128)])

@@ -78,7 +78,9 @@ def _step(state, ins, hazards=None):
     regs_here = set()
     for a in args:
         regs_here |= _vregs(a)
-    untracked = in_asm and (mnem.startswith("global_load") or mnem.startswith("ds_read"))
+    # An LDS DMA (global_load_lds_*) writes LDS, not registers: its first operand is the address.
+    lds_dma = mnem.startswith("global_load_lds")
+    untracked = in_asm and ((mnem.startswith("global_load") and not lds_dma) or mnem.startswith("ds_read"))
     dst = _vregs(args[0]) if (untracked and args) else set()
     bad = sorted(((regs_here - dst) | (dst if untracked else set())) & pending)
     if bad and hazards is not None:
@@ -184,6 +186,15 @@ def test_checker_flags_a_hoisted_use():
     ok = [";;#ASMSTART", "global_load_dwordx4 v[2:5], v[8:9], off", ";;#ASMEND",
           ";;#ASMSTART", "s_waitcnt vmcnt(0)", ";;#ASMEND", "v_permlane32_swap_b32_e32 v2, v4"]
     assert not check_kernel(ok)
+
+
+def test_checker_treats_lds_dma_operands_as_inputs():
+    """An asm LDS DMA's VGPR operand is its address (reusable at once); an asm register load's
+    first operand is a destination (pending until its wait)."""
+    dma = [";;#ASMSTART", "s_mov_b32 m0, s4", "global_load_lds_dword v7, s[2:3]", ";;#ASMEND", "v_xor_b32_e32 v8, 4, v7"]
+    assert not check_kernel(dma)
+    reg = [";;#ASMSTART", "global_load_dword v7, v[2:3], off", ";;#ASMEND", "v_xor_b32_e32 v8, 4, v7"]
+    assert check_kernel(reg)
 
 
 def test_no_bit_cast_of_vector_element():

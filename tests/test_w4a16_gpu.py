@@ -353,6 +353,21 @@ def test_baseline_c4_prefill_full_size():
     assert torch.equal(gemm(Wt, xt[:1000].contiguous(), st), y[:1000])
 
 
+def test_golden_small_problem():
+    """The committed fixture tests/golden/small_problem.npz (M=5, N=64, K=512, G=64): the op on its
+    inputs against its oracle output, through decode and every forced prefill variant (bitwise
+    equal to each other)."""
+    torch = torch_cuda()
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "small_problem.npz"))
+    Wp, x, s = (torch.from_numpy(np.ascontiguousarray(d[k])).cuda() for k in ("Wp", "x", "scales"))
+    assert_close(gemm(Wp, x, s, variant=0), d["y_ref"])
+    ys = [gemm(Wp, x, s, variant=v) for v in PREFILL_VARIANTS]
+    for y in ys:
+        assert torch.equal(y, ys[0])
+    assert_close(ys[0], d["y_ref"])
+
+
 def test_decode_split_k_concurrent_streams():
     """Split-K decode calls enqueued alternately on two streams (overlapping in time) give the
     single-stream results bit for bit: each stream has its own counter buffer."""

@@ -25,21 +25,56 @@
 namespace {
 
 // Decode split-K counters.  Launches that share a counter buffer must not overlap in time
-// (w4a16.h), and work on different streams may overlap, so eager calls keep one buffer per
-// (device, stream): zeroed when created, left zero by every launch.  Under HIP graph capture the
-// buffer is allocated per call from the capture's memory pool and zeroed by a fill kernel that
-// the graph records, so every replay starts from zero counters and no buffer is shared between a
-// graph and eager work.  The returned tensor must stay alive until the launch is enqueued.
+// (w4a16.h), and work on different streams may overlap, so:
+//  * eager calls keep one buffer per (device, stream): zeroed when created, left zero by every
+//    launch;
+//  * a call made under HIP graph capture gets a slice of its own from a per-device pool that the
+//    first eager call on the device zeroed; a slice is never handed out again, so graph nodes and
+//    eager work never share counters, and every replay leaves its slice zero for the next one.
+//    A graph must not be replayed concurrently with itself (its nodes own their slices).
+//  * if the pool is missing (no eager call before the capture) or used up, the captured call
+//    allocates its counters from the capture's memory pool and zeroes them with a fill kernel
+//    that the graph records (correct, one extra graph node per such call).
+// The returned tensor must stay alive until the launch is enqueued.
+constexpr int64_t kCapturePoolSlots = 1 << 20;
+
+struct CapturePool {
+    at::Tensor buf;
+    int64_t next = 0;
+};
+
 std::mutex g_mu;
 std::map<std::pair<int, hipStream_t>, at::Tensor> g_counters;
+std::map<int, CapturePool> g_capture_pool;
 
-at::Tensor decode_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
+bool capturing(hipStream_t stream) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     TORCH_CHECK(hipStreamIsCapturing(stream, &st) == hipSuccess, "hipStreamIsCapturing failed");
-    const auto opts = like.options().dtype(torch::kInt32);
-    if (st != hipStreamCaptureStatusNone) return torch::zeros({(int64_t)slots}, opts);
-    const std::pair<int, hipStream_t> key{(int)like.device().index(), stream};
+    return st != hipStreamCaptureStatusNone;
+}
+
+// Called on every eager call: creates the device's capture pool once, outside any capture.
+void ensure_capture_pool(const at::Tensor& like) {
+    const int dev = (int)like.device().index();
     std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_capture_pool.count(dev))
+        g_capture_pool[dev].buf = torch::zeros({kCapturePoolSlots}, like.options().dtype(torch::kInt32));
+}
+
+at::Tensor decode_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
+    const auto opts = like.options().dtype(torch::kInt32);
+    const int dev = (int)like.device().index();
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (capturing(stream)) {
+        auto pit = g_capture_pool.find(dev);
+        if (pit != g_capture_pool.end() && pit->second.next + slots <= kCapturePoolSlots) {
+            at::Tensor slice = pit->second.buf.narrow(0, pit->second.next, slots);
+            pit->second.next += (slots + 63) / 64 * 64;          // 256-byte aligned slices
+            return slice;
+        }
+        return torch::zeros({(int64_t)slots}, opts);
+    }
+    const std::pair<int, hipStream_t> key{dev, stream};
     auto it = g_counters.find(key);
     if (it == g_counters.end())
         it = g_counters.emplace(key, torch::zeros({(int64_t)w4a16_max_counter_slots()}, opts)).first;
@@ -87,6 +122,7 @@ torch::Tensor w4a16_gemm(torch::Tensor Wp, torch::Tensor x, torch::Tensor scales
     hipStream_t stream = c10::hip::getCurrentHIPStream(dev).stream();
     torch::Tensor y = torch::empty({prob.M, prob.N}, x.options());
     if (y.numel() == 0) return y;
+    if (!capturing(stream)) ensure_capture_pool(x);
 
     torch::Tensor ws;
     void* ws_ptr = nullptr;
