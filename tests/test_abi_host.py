@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 17
+        assert 1 <= p.kernel <= 21
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -164,20 +164,23 @@ def test_prefill_plan_invariants(lib, M, N):
 
 PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128),
                  8: (32, 16), 9: (64, 16), 10: (32, 64), 11: (64, 64), 12: (32, 128), 13: (64, 128), 14: (32, 128),
-                 15: (32, 256), 16: (16, 64), 17: (16, 64)}
+                 15: (32, 256), 16: (16, 64), 17: (16, 64), 18: (64, 128), 19: (64, 256), 20: (128, 128),
+                 21: (256, 256)}
 
 
 @pytest.mark.parametrize("M,N,K,want", [
     (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
-    (2048, 14336, 4096, 5), (1024, 6144, 4096, 5),                          # >= 3/4 of the CUs: 128x256
-    (1024, 4096, 4096, 7), (1024, 4096, 14336, 7),                           # 128 tiles of 128x256: 128x128
+    (1024, 6144, 4096, 5),                                                   # >= 3/4 of the CUs: 128x256
+    (2048, 14336, 4096, 21), (512, 28672, 8192, 21), (2048, 6144, 4096, 21), # <= 2 rounds of 256x256 tiles
+    (1024, 4096, 4096, 20), (1024, 4096, 14336, 20),                         # 128 tiles of 128x256: 128x128
+    (512, 6144, 4096, 20), (256, 14336, 4096, 20), (128, 28672, 4096, 20),   # 128x128, four 128x32 waves
+    (128, 14336, 4096, 18), (512, 4096, 4096, 18), (64, 28672, 4096, 18),    # 64x128, four 64x32 waves
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
     (17, 4096, 14336, 17), (32, 6144, 4096, 17), (32, 14336, 4096, 17),     # token groups of 16
     (33, 4096, 4096, 17), (64, 4096, 4096, 17), (128, 4096, 14336, 17), (48, 14336, 4096, 17),
+    (128, 6144, 4096, 17),
     (32, 28672, 4096, 10),                                                   # token groups of 32
-    (128, 14336, 4096, 14), (512, 4096, 4096, 14), (96, 14336, 4096, 14),    # 2 blocks per wave, 3 pairs
-    (512, 6144, 4096, 12), (192, 14336, 4096, 12),                           # 2 blocks per wave, 2 pairs
-    (256, 14336, 4096, 7), (128, 28672, 4096, 7),                            # moderate sizes: 128x128 wide
+    (256, 4096, 14336, 14),                                                  # 2 blocks per wave, 3 pairs
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
@@ -189,7 +192,7 @@ def test_prefill_wide_selection(lib, M, N, K, want):
     tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
     assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4, 12: 4, 13: 4, 14: 4,
-                            15: 4, 16: 4, 17: 4}[p.kernel]
+                            15: 4, 16: 4, 17: 4, 18: 4, 19: 8, 20: 4, 21: 8}[p.kernel]
 
 
 def test_prefill_override(lib, monkeypatch):
@@ -292,3 +295,26 @@ def test_bandwidth_probe_loads_and_rejects_bad_arguments():
     assert cp(16, 32, 0, None) == 1
     assert cp(16, 32, 1000, None) == 1
     assert cp(16, 40, 1024, None) == 1
+
+
+def test_planner_occupancy_hook_covers_every_prefill_config(lib):
+    lib.w4a16_debug_prefill_occupancy.argtypes = [ctypes.c_int, ctypes.POINTER(Limits)]
+    occ = [lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(MI355X)) for cfg in range(1, 22)]
+    assert all(o >= 1 for o in occ), occ
+    assert lib.w4a16_debug_prefill_occupancy(0, ctypes.byref(MI355X)) == -1
+    assert lib.w4a16_debug_prefill_occupancy(22, ctypes.byref(MI355X)) == -1
+    older = Limits(256, 64 * 1024, 1024, 942)                # 64 KB of LDS per CU bounds every config
+    assert all(lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(older)) <= o for cfg, o in zip(range(1, 22), occ))
+
+
+@pytest.mark.parametrize("M,N,K,want", [
+    (1, 14336, 4096, (20, 1)), (4, 14336, 4096, (20, 1)), (8, 14336, 4096, (16, 1)), (16, 14336, 4096, (16, 1)),
+    (1, 4096, 14336, (29, 1)), (4, 4096, 14336, (29, 1)), (8, 4096, 14336, (19, 1)), (16, 4096, 14336, (20, 2)),
+    (1, 28672, 4096, (29, 1)), (4, 28672, 4096, (21, 1)),                    # fused gate/up: twice as wide
+    (16, 28672, 4096, (12, 1)),                                              # ring tiles would need two rounds
+    (16, 4096, 4096, (19, 1)), (16, 6144, 4096, (20, 1))])                   # qkv: 384 single-block rings = 2 rounds
+def test_decode_selection(lib, M, N, K, want):
+    """The decode shapes the planner picks for the Llama-3 projections (BASELINE configs[1] first)."""
+    rc, p, err = plan(lib, M=M, N=N, K=K, G=128)
+    assert rc == 0, err
+    assert (p.decode_variant, p.splits) == want

@@ -237,13 +237,15 @@ def test_wide_prefill_accumulators_stay_in_place(isa):
     copies or AGPR<->VGPR transfers (the default scheduler's allocation rotated them through
     copies, serialising the MFMA pipe)."""
     ks = {k: v for k, v in _kernels(isa).items() if "prefill_wide_kernel" in k}
-    assert len(ks) == 3, list(ks)
+    assert len(ks) == 7, list(ks)
     for name, lines in ks.items():
+        bm, bn, wm, wn, _ = (int(v) for v in re.search(r"ILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)EE", name).groups())
+        tm, tn = bm // wm // 32, bn // wn // 32
         loops = [l for l in _loop_bodies(lines) if any("v_mfma" in t for t in l)]
         assert len(loops) == 1, (name, len(loops))
         ops = [t.split()[0] for t in loops[0]]
-        # two chunks of a 128 x 64 wave tile = 128 16x16x32 MFMAs' work (a 32x32x16 counts twice)
+        # two chunks of a (32 tm) x (32 tn) wave tile = 16 tm tn 16x16x32 MFMAs' work (a 32x32x16 counts twice)
         work = ops.count("v_mfma_f32_16x16x32_f16") + 2 * ops.count("v_mfma_f32_32x32x16_f16")
-        assert work == 128, (name, work)
+        assert work == 16 * tm * tn, (name, work)
         moves = [o for o in ops if o.startswith("v_accvgpr")]
         assert not moves, (name, len(moves))

@@ -291,7 +291,11 @@ def test_wide_prefill_32x32_index_math(M, N, K, G, BM, BN, WMs, WNs):
     assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-12
 
 
-@pytest.mark.parametrize("cfg", [5, 6, 7])
+WIDE_TILES = {5: (128, 256, 1, 4), 6: (256, 128, 2, 2), 7: (128, 128, 1, 2), 18: (64, 128, 1, 4), 19: (64, 256, 1, 8),
+              20: (128, 128, 1, 4), 21: (256, 256, 2, 4)}
+
+
+@pytest.mark.parametrize("cfg", sorted(WIDE_TILES))
 @pytest.mark.parametrize("M,N,K,G", [(300, 1040, 2048, 64), (129, 272, 1152, 64), (300, 80, 640, 64),
                                      (513, 208, 384, 128), (70, 16, 128, 64), (40, 4112, 4160, 64)])
 def test_wide_prefill_addresses_in_bounds(cfg, M, N, K, G):
@@ -299,7 +303,7 @@ def test_wide_prefill_addresses_in_bounds(cfg, M, N, K, G):
     whose last N tile is partial.  Regression: a per-lane block offset taken relative to an
     unclamped base went negative and, as the unsigned 32-bit offset of a saddr load, addressed
     4 GB past the weights."""
-    BM, BN, WMs, WNs = {5: (128, 256, 1, 4), 6: (256, 128, 2, 2), 7: (128, 128, 1, 2)}[cfg]
+    BM, BN, WMs, WNs = WIDE_TILES[cfg]
     NT, WM, WN = WMs * WNs * 64, BM // WMs, BN // WNs
     TM, TN = WM // 32, WN // 32
     KC, NBLK, gshift = K // 64, N // 16, 1 if G == 128 else 0

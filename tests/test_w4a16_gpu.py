@@ -505,10 +505,11 @@ def _onehot_decode_check(Wp, scales, Wd, K, v, splits, m):
     assert torch.equal(gemm(Wp, xo, scales, variant=0), gemm(Wp, xo, scales, variant=0))
 
 
-# Wide-tile prefill configs (5..7, chosen automatically for large problems) forced through
-# W4A16_PREFILL: bit-identical to the reference-API variants and within the reference tolerance,
-# including M and N tails (rows past M and blocks past N load clamped data and are not stored).
-@pytest.mark.parametrize("cfg", [5, 6, 7])
+# Wide-tile prefill configs (5..7 and 18..21, chosen automatically for moderate and large
+# problems) forced through W4A16_PREFILL: bit-identical to the reference-API variants and within
+# the reference tolerance, including M and N tails (rows past M and blocks past N load clamped
+# data and are not stored).
+@pytest.mark.parametrize("cfg", [5, 6, 7, 18, 19, 20, 21])
 @pytest.mark.parametrize("M,N,K,G", [(2048, 4096, 4096, 128), (300, 1040, 2048, 64), (129, 272, 1024, 128),
                                      (17, 16, 256, 64)])
 def test_prefill_wide_configs_bitwise_equal(cfg, M, N, K, G, monkeypatch):
@@ -582,3 +583,26 @@ def test_prefill_token_groups_bitwise_equal(monkeypatch, cfg, M, N, K, G):
     m = max(17, M // 3)                                       # M <= 16 would route to decode
     if m < M:
         assert torch.equal(gemm(Wp, x[:m].contiguous(), scales), y[:m])
+
+
+# The planner's occupancy table (resident workgroups per CU of each prefill config, which its
+# selection rules and fit checks use) agrees with the compiled kernels on this device.
+def test_planner_occupancy_matches_the_compiled_kernels():
+    import ctypes
+    import os
+    torch_cuda()
+    import w4a16_opt
+
+    class Limits(ctypes.Structure):
+        _fields_ = [("cu_count", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32),
+                    ("max_threads_per_block", ctypes.c_int32), ("gcn_arch", ctypes.c_int32)]
+
+    lib = ctypes.CDLL(os.path.join(PKG, "libw4a16_hip.so"))
+    lib.w4a16_debug_kernel_occupancy.argtypes = [ctypes.c_int]
+    lib.w4a16_debug_prefill_occupancy.argtypes = [ctypes.c_int, ctypes.POINTER(Limits)]
+    info = w4a16_opt.plan_info(2048, 4096, 4096, 128)
+    lim = Limits(info["cu_count"], info["lds_bytes_per_block"], 1024, info["gcn_arch"])
+    got = {cfg: lib.w4a16_debug_kernel_occupancy(cfg) for cfg in range(1, 22)}
+    planned = {cfg: lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(lim)) for cfg in range(1, 22)}
+    print("compiled occupancy:", got, flush=True)
+    assert got == planned

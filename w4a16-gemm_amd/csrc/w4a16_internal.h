@@ -7,37 +7,45 @@ namespace w4a16 {
 
 // Prefill tile configurations.  Ids 1..4 are the forced variants of the reference API (its
 // PfCfg<1..4>, src/vectorized/kernel.cu:59-63, re-tiled for 64-wide wavefronts and 256 CUs) and
-// run prefill_kernel (kind 0); ids 5..7 run prefill_wide_kernel (kind 1, wave tile 128 x 64);
-// ids 8..9 run prefill_stream_kernel (kind 2: one wave per n16 block over the whole K, for
-// M <= bm, ring of `depth` chunk pairs); ids 10..11 run prefill_group_kernel (kind 3: waves_n
-// waves, one per n16 block, share the x rows of a group of bm tokens in the ring; any M, one
-// token group per grid row).  The auto planner (or the W4A16_PREFILL override) picks among all
-// of them; all give bit-identical output.
+// run prefill_kernel (kind 0); ids 5..7 and 18..21 run prefill_wide_kernel (kind 1, 32x32x16
+// wave tiles of 64 or 128 tokens x 32 or 64 channels); ids 8..9 run prefill_stream_kernel (kind
+// 2: one wave per n16 block over the whole K, for M <= bm, ring of `depth` chunk pairs); ids
+// 10..17 run prefill_group_kernel (kind 3: waves_n waves, one or more n16 blocks each, share the
+// x rows of a group of bm tokens in the ring; any M, one token group per grid row).  The auto
+// planner (or the W4A16_PREFILL override) picks among all of them; all give bit-identical output.
+//   wpe: waves per SIMD the kind-1 kernels' registers are budgeted for (amdgpu_waves_per_eu);
+//   occ: resident workgroups per CU of the compiled kernel on gfx950 (registers, LDS and wave
+//        slots), the value hipOccupancyMaxActiveBlocksPerMultiprocessor reports for it
+//        (tests/test_w4a16_gpu.py::test_planner_occupancy_matches_the_compiled_kernels).
 struct PrefillTile {
-    int bm, bn, waves_m, waves_n, kind, depth;
+    int bm, bn, waves_m, waves_n, kind, depth, wpe, occ;
 };
-constexpr PrefillTile kPrefillTable[18] = {
-    {0, 0, 0, 0, 0, 0},
-    {16, 128, 1, 4, 0, 0},     // 1: small batches: 4 waves across N, wave tile 16 x 32
-    {32, 128, 1, 4, 0, 0},     // 2: wave tile 32 x 32
-    {64, 128, 2, 2, 0, 0},     // 3: wave tile 32 x 64
-    {128, 128, 2, 2, 0, 0},    // 4: wave tile 64 x 64
-    {128, 256, 1, 4, 1, 0},    // 5: wave tile 128 x 64, 4 waves across N
-    {256, 128, 2, 2, 1, 0},    // 6: wave tile 128 x 64, 2 x 2 waves
-    {128, 128, 1, 2, 1, 0},    // 7: wave tile 128 x 64, 2 waves
-    {32, 16, 1, 1, 2, 6},      // 8: M <= 32, one wave per n16 block, 6 pairs in flight
-    {64, 16, 1, 1, 2, 3},      // 9: M <= 64, one wave per n16 block, 3 pairs in flight
-    {32, 64, 1, 4, 3, 3},      // 10: groups of 32 tokens, 4 n16 blocks per workgroup, 3 pairs
-    {64, 64, 1, 4, 3, 2},      // 11: groups of 64 tokens, 4 n16 blocks per workgroup, 2 pairs
-    {32, 128, 1, 4, 3, 2},     // 12: groups of 32 tokens, 2 n16 blocks per wave, 2 pairs
-    {64, 128, 1, 4, 3, 2},     // 13: groups of 64 tokens, 2 n16 blocks per wave, 2 pairs (forced only)
-    {32, 128, 1, 4, 3, 3},     // 14: groups of 32 tokens, 2 n16 blocks per wave, 3 pairs
-    {32, 256, 1, 4, 3, 2},     // 15: groups of 32 tokens, 4 n16 blocks per wave, 2 pairs (forced only)
-    {16, 64, 1, 4, 3, 3},      // 16: groups of 16 tokens, 1 n16 block per wave, 3 pairs
-    {16, 64, 1, 4, 3, 4},      // 17: groups of 16 tokens, 1 n16 block per wave, 4 pairs
+constexpr PrefillTile kPrefillTable[22] = {
+    {0, 0, 0, 0, 0, 0, 0, 0},
+    {16, 128, 1, 4, 0, 0, 0, 7},     // 1: small batches: 4 waves across N, wave tile 16 x 32
+    {32, 128, 1, 4, 0, 0, 0, 6},     // 2: wave tile 32 x 32
+    {64, 128, 2, 2, 0, 0, 0, 3},     // 3: wave tile 32 x 64
+    {128, 128, 2, 2, 0, 0, 0, 2},    // 4: wave tile 64 x 64
+    {128, 256, 1, 4, 1, 0, 2, 2},    // 5: wave tile 128 x 64, 4 waves across N
+    {256, 128, 2, 2, 1, 0, 1, 1},    // 6: wave tile 128 x 64, 2 x 2 waves
+    {128, 128, 1, 2, 1, 0, 1, 2},    // 7: wave tile 128 x 64, 2 waves
+    {32, 16, 1, 1, 2, 6, 0, 2},      // 8: M <= 32, one wave per n16 block, 6 pairs in flight
+    {64, 16, 1, 1, 2, 3, 0, 2},      // 9: M <= 64, one wave per n16 block, 3 pairs in flight
+    {32, 64, 1, 4, 3, 3, 0, 3},      // 10: groups of 32 tokens, 4 n16 blocks per workgroup, 3 pairs
+    {64, 64, 1, 4, 3, 2, 0, 2},      // 11: groups of 64 tokens, 4 n16 blocks per workgroup, 2 pairs
+    {32, 128, 1, 4, 3, 2, 0, 3},     // 12: groups of 32 tokens, 2 n16 blocks per wave, 2 pairs
+    {64, 128, 1, 4, 3, 2, 0, 2},     // 13: groups of 64 tokens, 2 n16 blocks per wave, 2 pairs (forced only)
+    {32, 128, 1, 4, 3, 3, 0, 2},     // 14: groups of 32 tokens, 2 n16 blocks per wave, 3 pairs
+    {32, 256, 1, 4, 3, 2, 0, 2},     // 15: groups of 32 tokens, 4 n16 blocks per wave, 2 pairs (forced only)
+    {16, 64, 1, 4, 3, 3, 0, 4},      // 16: groups of 16 tokens, 1 n16 block per wave, 3 pairs
+    {16, 64, 1, 4, 3, 4, 0, 3},      // 17: groups of 16 tokens, 1 n16 block per wave, 4 pairs
+    {64, 128, 1, 4, 1, 0, 2, 3},     // 18: wave tile 64 x 32, 4 waves across N
+    {64, 256, 1, 8, 1, 0, 2, 2},     // 19: wave tile 64 x 32, 8 waves across N share the x rows
+    {128, 128, 1, 4, 1, 0, 2, 2},    // 20: wave tile 128 x 32, 4 waves across N
+    {256, 256, 2, 4, 1, 0, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 17;     // all prefill configs
+constexpr int kNumPrefillTable = 21;     // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;

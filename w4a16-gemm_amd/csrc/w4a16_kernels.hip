@@ -1080,6 +1080,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 // compiled with a different instruction-scheduling strategy.
 hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
                                uint16_t* y, hipStream_t st);
+int prefill_wide_occupancy(int cfg);
 
 template <int CFG> struct PrefillCfg;
 #define W4A16_PREFILL_CFG(ID)                                                                  \
@@ -1104,6 +1105,10 @@ W4A16_PREFILL_CFG(14)
 W4A16_PREFILL_CFG(15)
 W4A16_PREFILL_CFG(16)
 W4A16_PREFILL_CFG(17)
+W4A16_PREFILL_CFG(18)
+W4A16_PREFILL_CFG(19)
+W4A16_PREFILL_CFG(20)
+W4A16_PREFILL_CFG(21)
 #undef W4A16_PREFILL_CFG
 
 template <int CFG>
@@ -1124,6 +1129,27 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
         hipLaunchKernelGGL((prefill_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
                            dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
     return hipGetLastError();
+}
+
+// Resident workgroups per CU of a prefill config's compiled kernel (HIP occupancy query on the
+// current device), -1 on error.
+template <int CFG>
+static int prefill_occupancy_of() {
+    using C = PrefillCfg<CFG>;
+    int n = 0;
+    hipError_t e = hipSuccess;
+    if constexpr (kPrefillTable[CFG].kind == 3)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, prefill_group_kernel<C::BM / 16, kPrefillTable[CFG].depth, C::WN, C::BN / (16 * C::WN)>, 64 * C::WN, 0);
+    else if constexpr (kPrefillTable[CFG].kind == 2)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_stream_kernel<C::BM / 16, kPrefillTable[CFG].depth>,
+                                                         64, 0);
+    else if constexpr (kPrefillTable[CFG].kind == 1)
+        return prefill_wide_occupancy(CFG);
+    else
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<C::BM, C::BN, C::WM, C::WN>,
+                                                         C::WM * C::WN * 64, 0);
+    return e == hipSuccess ? n : -1;
 }
 
 template <int V>
@@ -1288,6 +1314,10 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
             case 15: e = launch_prefill<15>(p, wp, x, scales, y, st); break;
             case 16: e = launch_prefill<16>(p, wp, x, scales, y, st); break;
             case 17: e = launch_prefill<17>(p, wp, x, scales, y, st); break;
+            case 18: e = launch_prefill<18>(p, wp, x, scales, y, st); break;
+            case 19: e = launch_prefill<19>(p, wp, x, scales, y, st); break;
+            case 20: e = launch_prefill<20>(p, wp, x, scales, y, st); break;
+            case 21: e = launch_prefill<21>(p, wp, x, scales, y, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }
@@ -1296,4 +1326,33 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
         return W4A16_ERR_HIP;
     }
     return W4A16_OK;
+}
+
+// Test hook (no counterpart in the reference): the compiled occupancy of prefill config `cfg`
+// on the current device, which the planner's table must match.
+extern "C" int w4a16_debug_kernel_occupancy(int cfg) {
+    switch (cfg) {
+        case 1: return prefill_occupancy_of<1>();
+        case 2: return prefill_occupancy_of<2>();
+        case 3: return prefill_occupancy_of<3>();
+        case 4: return prefill_occupancy_of<4>();
+        case 5: return prefill_occupancy_of<5>();
+        case 6: return prefill_occupancy_of<6>();
+        case 7: return prefill_occupancy_of<7>();
+        case 8: return prefill_occupancy_of<8>();
+        case 9: return prefill_occupancy_of<9>();
+        case 10: return prefill_occupancy_of<10>();
+        case 11: return prefill_occupancy_of<11>();
+        case 12: return prefill_occupancy_of<12>();
+        case 13: return prefill_occupancy_of<13>();
+        case 14: return prefill_occupancy_of<14>();
+        case 15: return prefill_occupancy_of<15>();
+        case 16: return prefill_occupancy_of<16>();
+        case 17: return prefill_occupancy_of<17>();
+        case 18: return prefill_occupancy_of<18>();
+        case 19: return prefill_occupancy_of<19>();
+        case 20: return prefill_occupancy_of<20>();
+        case 21: return prefill_occupancy_of<21>();
+        default: return -1;
+    }
 }

@@ -7,6 +7,7 @@
 // which owns the tensors.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -43,21 +44,17 @@ bool debug_enabled() {
 
 // LDS per CU: 160 KB on gfx950 (CDNA4), 64 KB on earlier CDNA parts.
 int lds_per_cu(const w4a16_device_limits& lim) {
-    return lim.gcn_arch >= 950 ? 160 * 1024 : 64 * 1024;
+    return lim.gcn_arch == 950 ? 160 * 1024 : 64 * 1024;
 }
 
-// Resident workgroups per CU for a prefill config (LDS- and wave-slot-limited estimate;
-// registers are budgeted so that two workgroups of any config fit).
+// Resident workgroups per CU for a prefill config: the compiled kernel's occupancy on gfx950
+// (the table's occ field, which a GPU test checks against the HIP occupancy query), bounded by
+// the device's LDS per CU; 0 when the config does not fit the device at all.
 int prefill_occupancy(int cfg, const w4a16_device_limits& lim) {
     const int lds = prefill_lds_bytes(cfg);
     if (lds > lim.lds_bytes_per_block) return 0;
     if (prefill_threads(cfg) > lim.max_threads_per_block) return 0;
-    int occ = lds_per_cu(lim) / lds;
-    const int waves = kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n;
-    occ = std::min(occ, 32 / waves);      // 8 wave slots per SIMD x 4 SIMDs
-    occ = std::min(occ, 2);               // VGPR budget (acc + operands) of the larger tiles
-    if (kPrefillTable[cfg].kind == 1) occ = std::min(occ, std::max(1, 4 / waves));   // ~320 registers: 1 wave/SIMD
-    return std::max(occ, 0);
+    return std::max(0, std::min(kPrefillTable[cfg].occ, lds_per_cu(lim) / lds));
 }
 
 // Auto prefill selection (replaces pf_select, kernel.cu:142-156).  Cost = full-device waves of
@@ -76,28 +73,34 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         const double tiles = std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn);
         return tiles <= (double)std::numeric_limits<int32_t>::max() ? tiles : -1.0;
     };
-    // Rules measured on MI355X (graph-timed sweep of every config over M = 17..1024 on the
-    // Llama-3-8B projection shapes):
+    // Rules measured on MI355X (w4a16-gemm_amd/route_sweep.py: every config forced, graph-timed,
+    // on the Llama-3-8B projections and the BASELINE shapes, M = 17..2048):
+    //  * the wide 32x32x16 tiles first, largest first, once their tiles number at least 3/4 of
+    //    the CUs and the M tile is filled: 256 x 256 (8 waves, wave tile 128 x 64) while at most
+    //    two rounds of them (M = 256..2048), e.g. N = 28672, K = 8192, M = 512: 230 vs 241 us
+    //    for 128 x 256; then 128 x 256 (two workgroups per CU); then 128 x 128 with four waves
+    //    of 128 x 32 (M >= 128), e.g. N = 28672, M = 128: 43.4 vs 55.4 us for two waves of
+    //    128 x 64, N = 4096, K = 14336, M = 1024: 137 vs 171; then 64 x 128 with four waves of
+    //    64 x 32 (M >= 64), e.g. configs[2] (M = 128, N = 14336, G = 64): 29.9 vs 36.4 us for
+    //    token groups of 32, N = 4096, M = 512: 29.4 vs 34.1;
     //  * token groups of 16 rows, one n16 block per wave, 4 pairs in flight, while their waves
     //    (M/16 groups x N/16 blocks) are at most 12 per CU: every small-M shape measured, e.g.
     //    K = 14336, N = 4096, M = 32: 42.8 vs 52.6 us for one wave per block over 32 rows
-    //    (prefill_stream_kernel, now forced-only); M = 128: 50 vs 59 us for groups of 32;
+    //    (prefill_stream_kernel, now forced-only);
     //  * token groups of 32 rows with two n16 blocks per wave (every x operand read feeds two
     //    MFMAs) while their waves (M/32 groups x N/32 block pairs) number 4..12 per CU, 3 pairs
-    //    in flight up to 8 per CU, else 2: e.g. M = 128, N = 14336: 32.9 vs 45.7 us;
-    //    M = 512, N = 6144: 46.4 vs 53.8 us for 128 x 128 tiles;
+    //    in flight up to 8 per CU, else 2;
     //  * token groups of 32 rows, one n16 block per wave, while the waves (M/32 groups x N/16
-    //    blocks) are at most 12 per CU: e.g. K = 14336, N = 4096, M = 128: 60 vs 77 us with two
-    //    blocks per wave (too few waves); N = 28672, M = 32: 25.6 vs 49 us;
-    //  * token groups of 64 rows while those waves are at most 8 per CU (N = 4096, M = 512: 43 vs
-    //    46 us; N = 28672, M = 64: 45 vs 50 us);
-    //  * then the wide tiles, which beat the 16..128-row tiles for every larger size measured
-    //    (N = 6144, M = 512: 54 vs 73 us): 128 x 256 tiles (two workgroups per CU) once they
-    //    number at least 3/4 of the CUs, else 128 x 128 tiles.  Forced-config sweep, K = 4096
-    //    unless noted: 128 x 256 vs 128 x 128 at N = 6144, M = 1024 (192 tiles): 62.2 vs 66.6 us;
-    //    M = 2048: 116.1 vs 129.5; N = 28672, M = 512: 133.2 vs 139.9, M = 1024: 245.0 vs 269.0;
-    //    N = 4096, M = 2048: 73.9 vs 78.6; at 128 tiles 128 x 128 wins (N = 4096, M = 1024: 57.9
-    //    vs 53.7 us; K = 14336: 183.3 vs 170.5).  256 x 128 tiles lost everywhere.
+    //    blocks) are at most 12 per CU: e.g. N = 28672, M = 32: 25.6 vs 49 us;
+    //  * token groups of 64 rows while those waves are at most 8 per CU;
+    //  * else the 128 x 128 wide tiles.
+    if (M >= 256 && M <= 2048) {
+        const double t = wide_tiles(21);
+        if (t >= 0.75 * cus && t <= 2.0 * cus) return 21;
+    }
+    if (wide_tiles(5) >= 0.75 * cus) return 5;
+    if (M >= 128 && wide_tiles(20) >= 0.75 * cus) return 20;
+    if (M >= 64 && wide_tiles(18) >= 0.75 * cus) return 18;
     const double blocks = std::ceil(N / 16.0);
     if (prefill_occupancy(17, lim) > 0 && prefill_shape_ok(17, M, K) &&
         std::ceil(M / 16.0) * blocks <= 12.0 * cus)
@@ -113,8 +116,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     if (prefill_occupancy(11, lim) > 0 && prefill_shape_ok(11, M, K) &&
         std::ceil(M / 64.0) * blocks <= 8.0 * cus)
         return 11;
-    if (wide_tiles(5) >= 0.75 * cus) return 5;
-    if (wide_tiles(7) > 0) return 7;
+    if (wide_tiles(20) > 0) return 20;
     for (int cfg = kNumPrefillTable; cfg >= 1; --cfg) {    // descending: ties go to the later config
         const int occ = prefill_occupancy(cfg, lim);
         if (occ < 1 || !prefill_shape_ok(cfg, M, K) || kPrefillTable[cfg].kind >= 1) continue;   // other kinds: rules above
@@ -133,6 +135,12 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
 extern "C" void w4a16_set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
 extern "C" const char* w4a16_last_error(void) { return g_last_error.c_str(); }
 extern "C" int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
+
+// Test hook (no counterpart in the reference): the planner's occupancy for prefill config `cfg`.
+extern "C" int w4a16_debug_prefill_occupancy(int cfg, const w4a16_device_limits* lim) {
+    if (!lim || cfg < 1 || cfg > kNumPrefillTable) return -1;
+    return prefill_occupancy(cfg, *lim);
+}
 extern "C" int32_t w4a16_max_counter_slots(void) { return kMaxCounterSlots; }
 
 extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w4a16_device_limits* lim,
@@ -191,36 +199,51 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             }
         }
         if (var < 0) {
-            // Shapes measured fastest on MI355X (graph-timed sweep over the whole table) for the
-            // Llama-3 decode projections, tried in order; the first that fits wins:
+            // Shapes measured fastest on MI355X (graph-timed sweeps over the whole table,
+            // w4a16-gemm_amd/route_sweep.py) for the Llama-3 decode projections, tried in order;
+            // the first that fits wins:
             //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): refill-ahead
             //    rings of 4 waves, 2 blocks while the x rows are few (M <= 4), else 4 blocks; no
-            //    split;
+            //    split.  Twice as wide (fused gate/up, N = 28672): single-block rings of 8 waves
+            //    at M = 1 (14.6 vs 16.8 us), of 4 waves with 4 pairs in flight at M <= 4;
             //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves,
             //    3 pairs in flight up to 4 token rows and 2 up to 8 rows; above 8 rows, where the x
             //    traffic per block grows, two-block tiles of 4 waves split in two (M = 16: 11.95
             //    vs 12.57 us for 8 waves, in two sweeps);
-            //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves.
+            //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves, else two-block
+            //    rings of 4.
+            // Above 8 token rows a ring's LDS allows one or two workgroups per CU, so a shape is
+            // taken only if all its workgroups are resident at once (qkv, N = 6144, M = 16: 6.7
+            // vs 9.4 us for the single-block rings, whose 384 workgroups ran in two rounds).
             auto ok = [&](int cand, int sp) {
                 return decode_shape_fits(cand, KC, sp, G) && decode_lds_bytes(cand, M) <= lim->lds_bytes_per_block &&
                        kDecodeTable[cand].waves * 64 <= lim->max_threads_per_block;
             };
             auto ntiles_of = [&](int cand) { return N / (16 * kDecodeTable[cand].nbw); };
+            auto one_round = [&](int cand, int sp) {
+                const int per_cu = std::min(lds_per_cu(*lim) / decode_lds_bytes(cand, M), 32 / kDecodeTable[cand].waves);
+                return (int64_t)ntiles_of(cand) * sp <= (int64_t)per_cu * cus;
+            };
             struct Cand { int v, sp; };
+            Cand vwide_m1[] = {{29, 1}, {20, 1}, {12, 1}};
+            Cand vwide_small_m[] = {{21, 1}, {20, 1}, {12, 1}};
             Cand wide_small_m[] = {{20, 1}, {12, 1}, {7, 1}};
             Cand wide[] = {{16, 1}, {12, 1}, {7, 1}};
             Cand longk_m4[] = {{29, 1}, {19, 1}, {22, 2}};
             Cand longk_small_m[] = {{19, 1}, {22, 2}, {22, 2}};
             Cand longk_large_m[] = {{20, 2}, {22, 2}, {19, 1}};
             Cand shortk_m1[] = {{29, 1}, {19, 1}, {14, 1}};
-            Cand shortk[] = {{19, 1}, {21, 1}, {21, 1}};
+            Cand shortk[] = {{19, 1}, {20, 1}, {21, 1}};
             Cand* list;
             const int n = 3;
-            if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus) list = M <= 4 ? wide_small_m : wide;
+            const bool very_wide = (int64_t)ntiles_of(12) * 2 >= 3LL * cus;
+            if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus)
+                list = M <= 1 && very_wide ? vwide_m1 : M <= 4 ? (very_wide ? vwide_small_m : wide_small_m) : wide;
             else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
             else list = M <= 1 ? shortk_m1 : shortk;
             for (int i = 0; i < n && var < 0; ++i)
-                if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus) {
+                if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus &&
+                    (M <= 8 || one_round(list[i].v, list[i].sp))) {
                     var = list[i].v; splits = list[i].sp;
                 }
             if (var < 0 && KC >= 128) {

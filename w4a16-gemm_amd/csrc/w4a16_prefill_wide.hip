@@ -1,4 +1,4 @@
-// Wide-tile prefill (configs 5..7 of kPrefillTable, kind 1) in its own translation unit.
+// Wide-tile prefill (configs 5..7 and 18..21 of kPrefillTable, kind 1) in its own translation unit.
 //
 // Built with -mllvm -amdgpu-sched-strategy=max-memory-clause (build.py): with the default
 // scheduler the register allocator gives most MFMAs a destination other than their accumulator
@@ -48,18 +48,16 @@ namespace w4a16 {
 //    and their weight tiles.  Measured on configs[3] (M = 2048, 16 M tiles): group_m = 4 fetches
 //    0.94 GB per launch from beyond L2 against 2.01 GB with all 16 M tiles of a weight tile
 //    first, and runs 2-3% faster (931 vs 953-962 us); 2 and 8 are within 1% of 4.
-// Waves per SIMD the wide kernels are compiled for.  128 x 256 tiles (1 x 4 waves): 2, i.e. two
-// workgroups per CU, so one workgroup's MFMAs run while the other dequantises, stages x and
-// waits at its barrier (at 1, the default for its 328 registers, the matrix cores idled ~48% of
-// the time).  The compiler then keeps the 128 accumulators in VGPRs and spills three registers
-// outside the loop.  The other shapes stay at 1: at 2, 256 x 128 spills 67 times inside its loop
-// and 128 x 128 spills a pending asm-load destination (tests/test_isa_hazards.py rejects that).
-template <int WAVES_M, int WAVES_N>
-constexpr int kWideWavesPerEu = WAVES_M == 1 && WAVES_N == 4 ? 2 : 1;
-
-template <int BM, int BN, int WAVES_M, int WAVES_N>
-__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
-__attribute__((amdgpu_waves_per_eu(kWideWavesPerEu<WAVES_M, WAVES_N>, kWideWavesPerEu<WAVES_M, WAVES_N>)))
+// Waves per SIMD the wide kernels' registers are budgeted for (WPE, the table's wpe field).
+// 128 x 256 tiles (1 x 4 waves): 2, i.e. two workgroups per CU, so one workgroup's MFMAs run
+// while the other dequantises, stages x and waits at its barrier (at 1, the default for its 328
+// registers, the matrix cores idled ~48% of the time).  The compiler then keeps the 128
+// accumulators in VGPRs and spills three registers outside the loop.  256 x 128 and 128 x 128
+// (1 x 2) stay at 1: at 2, 256 x 128 spills 67 times inside its loop and 128 x 128 spills a
+// pending asm-load destination (tests/test_isa_hazards.py rejects that).  The 32-channel wave
+// tiles (configs 18..20) and the 8-wave 256 x 256 tile fit 2 without spills.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE>
+__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
                     int M, int N, int K, int gshift, int tiles_m, int group_m) {
@@ -292,7 +290,7 @@ static hipError_t launch_wide(const w4a16_plan& p, const u4* Wp, const uint16_t*
         const int g = std::atoi(o);
         if (g >= 1) group_m = std::min(g, tiles_m);
     }
-    hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n>), dim3(p.grid),
+    hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe>), dim3(p.grid),
                        dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
                        group_m);
     return hipGetLastError();
@@ -304,7 +302,36 @@ hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const
         case 5: return launch_wide<5>(p, Wp, x, s, y, st);
         case 6: return launch_wide<6>(p, Wp, x, s, y, st);
         case 7: return launch_wide<7>(p, Wp, x, s, y, st);
+        case 18: return launch_wide<18>(p, Wp, x, s, y, st);
+        case 19: return launch_wide<19>(p, Wp, x, s, y, st);
+        case 20: return launch_wide<20>(p, Wp, x, s, y, st);
+        case 21: return launch_wide<21>(p, Wp, x, s, y, st);
         default: return hipErrorInvalidValue;
+    }
+}
+
+// Resident workgroups per CU of a wide config's compiled kernel (HIP occupancy query), -1 on
+// error; a test hook that checks the planner's table.
+template <int CFG>
+static int occupancy_wide() {
+    constexpr PrefillTile c = kPrefillTable[CFG];
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe>,
+                                                     c.waves_m * c.waves_n * 64, 0) != hipSuccess)
+        return -1;
+    return n;
+}
+
+int prefill_wide_occupancy(int cfg) {
+    switch (cfg) {
+        case 5: return occupancy_wide<5>();
+        case 6: return occupancy_wide<6>();
+        case 7: return occupancy_wide<7>();
+        case 18: return occupancy_wide<18>();
+        case 19: return occupancy_wide<19>();
+        case 20: return occupancy_wide<20>();
+        case 21: return occupancy_wide<21>();
+        default: return -1;
     }
 }
 

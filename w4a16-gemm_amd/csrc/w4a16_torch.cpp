@@ -201,9 +201,10 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
             d["kernel_name"] = tmpl("prefill_stream_kernel", {t.bm / 16, t.depth});
         else if (t.kind == 3)
             d["kernel_name"] = tmpl("prefill_group_kernel", {t.bm / 16, t.depth, t.waves_n, t.bn / (16 * t.waves_n)});
+        else if (t.kind == 1)
+            d["kernel_name"] = tmpl("prefill_wide_kernel", {t.bm, t.bn, t.waves_m, t.waves_n, t.wpe});
         else
-            d["kernel_name"] = tmpl(t.kind == 1 ? "prefill_wide_kernel" : "prefill_kernel",
-                                    {t.bm, t.bn, t.waves_m, t.waves_n});
+            d["kernel_name"] = tmpl("prefill_kernel", {t.bm, t.bn, t.waves_m, t.waves_n});
     }
     d["cu_count"] = lim.cu_count; d["gcn_arch"] = lim.gcn_arch; d["lds_bytes_per_block"] = lim.lds_bytes_per_block;
     return d;
