@@ -70,13 +70,15 @@ typedef struct w4a16_device_limits {
 /* A launch plan: the result of validation + routing + selection.  Plain data; copyable. */
 typedef struct w4a16_plan {
     int32_t M, N, K, G;
-    int32_t kernel;           /* 0 = decode, 1..4 = prefill tile config                 */
-    int32_t splits;           /* decode: number of K ranges reduced across workgroups    */
-    int32_t slab_chunks;      /* decode: 64-wide K chunks per wave                       */
+    int32_t kernel;           /* 0 = decode, 1..21 = prefill tile config (1..4 forced)   */
+    int32_t splits;           /* K ranges reduced across workgroups (decode split-K;
+                                 prefill token-group configs: the K segments, K > 8192)  */
+    int32_t slab_chunks;      /* decode: 64-wide K chunks per wave; prefill: chunks per
+                                 K segment of the fixed accumulation order               */
     int32_t tile_n;           /* decode: output columns per workgroup                    */
     int32_t grid;             /* workgroups launched by the main kernel                  */
     int32_t block;            /* threads per workgroup                                   */
-    int32_t counter_slots;    /* ints of the counter buffer used (decode split-K fixup)  */
+    int32_t counter_slots;    /* ints of the counter buffer used (split-K fixup)         */
     int32_t decode_variant;   /* decode: kernel shape id (waves, n16 blocks per wave)     */
     uint64_t workspace_bytes; /* bytes of fp32 partials the launch needs (0 if none)     */
 } w4a16_plan;

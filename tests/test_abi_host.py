@@ -177,10 +177,11 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (128, 14336, 4096, 18), (512, 4096, 4096, 18), (64, 28672, 4096, 18),    # 64x128, four 64x32 waves
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
     (17, 4096, 14336, 17), (32, 6144, 4096, 17), (32, 14336, 4096, 17),     # token groups of 16
-    (33, 4096, 4096, 17), (64, 4096, 4096, 17), (128, 4096, 14336, 17), (48, 14336, 4096, 17),
-    (128, 6144, 4096, 17),
+    (33, 4096, 4096, 17), (64, 4096, 4096, 17), (48, 14336, 4096, 17), (128, 6144, 4096, 17),
     (32, 28672, 4096, 10),                                                   # token groups of 32
-    (256, 4096, 14336, 14),                                                  # 2 blocks per wave, 3 pairs
+    # long K (4 or 7 segments): split-K token groups, larger groups sooner
+    (64, 4096, 14336, 10), (128, 4096, 14336, 12), (256, 4096, 14336, 13), (512, 4096, 14336, 18),
+    (17, 8192, 28672, 12), (192, 8192, 28672, 13), (384, 8192, 28672, 19), (2048, 8192, 28672, 20),
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
@@ -190,7 +191,7 @@ def test_prefill_wide_selection(lib, M, N, K, want):
     else:
         assert p.kernel == want
     tiles = PREFILL_TILES[p.kernel]
-    assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1])
+    assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1]) * max(p.splits, 1)
     assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4, 12: 4, 13: 4, 14: 4,
                             15: 4, 16: 4, 17: 4, 18: 4, 19: 8, 20: 4, 21: 8}[p.kernel]
 
@@ -318,3 +319,47 @@ def test_decode_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=128)
     assert rc == 0, err
     assert (p.decode_variant, p.splits) == want
+
+
+@pytest.mark.parametrize("M,N,K", [(32, 4096, 14336), (17, 4096, 14336), (100, 4096, 8320), (64, 8192, 28672)])
+def test_long_k_plans_split_token_group_configs_by_segment(lib, monkeypatch, M, N, K):
+    """K > 8192: the token-group (kind 3) and one-wave (kind 2) configs run one canonical K
+    segment per workgroup (grid = tiles x segments, one counter per tile, fp32 partials of every
+    segment); the other kinds keep the segments in-kernel (no workspace)."""
+    KC = K // 64
+    s = -(-KC // 64)
+    L = 2 * -(-KC // (2 * s))
+    segs = -(-KC // L)
+    for cfg, kind in [(17, 3), (14, 3), (9, 2), (4, 0), (18, 1), (20, 1)]:
+        monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+        rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
+        assert rc == 0, err
+        if p.kernel != cfg:                        # the config does not fit this shape
+            assert cfg in (9, 4, 18, 20) and (cfg != 9 or M > 64), (cfg, p.kernel)
+            continue
+        bm, bn = PREFILL_TILES[cfg]
+        tiles = -(-M // bm) * -(-N // bn)
+        assert p.slab_chunks == L
+        if kind >= 2:
+            assert (p.splits, p.grid, p.counter_slots, p.workspace_bytes) == (segs, tiles * segs, tiles, segs * M * N * 4)
+        else:
+            assert (p.splits, p.grid, p.counter_slots, p.workspace_bytes) == (1, tiles, 0, 0)
+    monkeypatch.setenv("W4A16_PREFILL", "5")       # 128 x 256 tiles: no registers for the second set
+    rc, p, err = plan(lib, M=2048, N=4096, K=14336, G=128)
+    assert rc == 0 and p.kernel != 5
+
+
+def test_canonical_segments():
+    """The segment rule of the accumulation order: one chain up to K = 8192, then balanced even
+    segments of at most 64 chunks; every segment non-empty."""
+    def segs(KC):
+        if KC <= 128:
+            return KC, 1
+        s = -(-KC // 64)
+        L = 2 * -(-KC // (2 * s))
+        return L, -(-KC // L)
+    assert segs(64) == (64, 1) and segs(128) == (128, 1)
+    assert segs(224) == (56, 4) and segs(448) == (64, 7) and segs(130) == (44, 3)
+    for KC in range(129, 5000):
+        L, S = segs(KC)
+        assert L % 2 == 0 and L <= 64 + 1 and 0 < KC - (S - 1) * L <= L

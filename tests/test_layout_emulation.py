@@ -523,3 +523,30 @@ def test_wide_prefill_grouped_tile_order_is_a_bijection(tiles_m, tiles_n, group_
         assert 0 <= tm < tiles_m and 0 <= tn < tiles_n
         seen.add((tm, tn))
     assert len(seen) == G
+
+
+@pytest.mark.parametrize("groups_m,cols,KC,D", [(2, 64, 224, 4), (3, 4, 130, 3), (1, 7, 448, 2), (5, 13, 192, 3)])
+def test_group_split_k_covers_every_tile_segment_and_pair(groups_m, cols, KC, D):
+    """prefill_group_kernel at K > 8192: block b -> (segment, tile) after the XCD remap visits every
+    (segment, tile) once, and the segments' pair ranges [pair0, pair0 + npair) tile [0, KC/2) with
+    at least D pairs each (the ring's prologue issues D pairs), so every load stays in the weights."""
+    L = KC if KC <= 128 else 2 * -(-KC // (2 * -(-KC // 64)))
+    splits = -(-KC // L)
+    seg_pairs = L // 2
+    tiles = groups_m * cols
+    G = tiles * splits
+    G8 = G >> 3
+    seen = set()
+    for b in range(G):
+        tile_raw = (b & 7) * G8 + (b >> 3) if b < (G8 << 3) else b
+        seg, tile = tile_raw // tiles, tile_raw % tiles
+        assert 0 <= seg < splits and 0 <= tile < tiles
+        seen.add((seg, tile))
+    assert len(seen) == G
+    covered = []
+    for seg in range(splits):
+        pair0 = seg * seg_pairs
+        npair = min(seg_pairs, KC // 2 - pair0)
+        assert npair >= D
+        covered += list(range(pair0, pair0 + npair))
+    assert covered == list(range(KC // 2))

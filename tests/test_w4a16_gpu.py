@@ -368,12 +368,14 @@ def test_golden_small_problem():
     assert_close(ys[0], d["y_ref"])
 
 
-def test_decode_split_k_concurrent_streams():
-    """Split-K decode calls enqueued alternately on two streams (overlapping in time) give the
-    single-stream results bit for bit: each stream has its own counter buffer."""
+@pytest.mark.parametrize("M", [16, 40])
+def test_decode_split_k_concurrent_streams(M):
+    """Split-K calls (decode at M = 16, the long-K prefill segments at M = 40) enqueued
+    alternately on two streams (overlapping in time) give the single-stream results bit for bit:
+    each stream has its own counter buffer."""
     torch = torch_cuda()
     import w4a16_opt
-    M, N, K, G = 16, 256, 14336, 128
+    N, K, G = 256, 14336, 128
     info = w4a16_opt.plan_info(M, N, K, G)
     assert info["splits"] > 1, info
     _, q, scales, Wp, key = make_problem(M, N, K, G, seed=41)
@@ -393,13 +395,13 @@ def test_decode_split_k_concurrent_streams():
     assert_close(want[0], ref_gemm(xs[0], q, scales, G, key))
 
 
-def test_cuda_graph_capture_split_k():
-    """Graph capture of a split-K decode plan with no eager call on the capture stream first:
-    the counters come from the capture's pool, zeroed inside the graph; every replay (with eager
-    split-K calls between them) equals the eager result."""
+@pytest.mark.parametrize("M", [12, 33])
+def test_cuda_graph_capture_split_k(M):
+    """Graph capture of a split-K plan (decode at M = 12, long-K prefill segments at M = 33):
+    every replay (with eager split-K calls between them) equals the eager result."""
     torch = torch_cuda()
     import w4a16_opt
-    M, N, K, G = 12, 256, 14336, 128
+    N, K, G = 256, 14336, 128
     assert w4a16_opt.plan_info(M, N, K, G)["splits"] > 1
     x, q, scales, Wp, key = make_problem(M, N, K, G, seed=43)
     g = torch.cuda.CUDAGraph()
@@ -606,3 +608,34 @@ def test_planner_occupancy_matches_the_compiled_kernels():
     planned = {cfg: lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(lim)) for cfg in range(1, 22)}
     print("compiled occupancy:", got, flush=True)
     assert got == planned
+
+
+# Long K (K > 8192) uses the canonical segmented accumulation order (w4a16_internal.h): the
+# token-group and one-wave configs run one K segment per workgroup and add the fp32 partials in
+# segment order, the others keep a second accumulator set.  Every config gives the same bits as
+# the reference-API variants, rows are independent of M, and the result is within tolerance.
+@pytest.mark.parametrize("M,N,K,G", [(32, 4096, 14336, 128), (100, 272, 8320, 64), (17, 512, 28672, 128),
+                                     (300, 1040, 12288, 64)])
+def test_long_k_segmented_order_bitwise_equal_across_configs(M, N, K, G, monkeypatch):
+    torch = torch_cuda()
+    import w4a16_opt
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=M + 7)
+    want = gemm(Wp, x, scales, variant=4)
+    assert_close(want, ref_gemm(x, q, scales, G, key))
+    seen = []
+    for cfg in range(1, 22):
+        monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+        info = w4a16_opt.plan_info(M, N, K, G)
+        if info["kernel"] != cfg:
+            continue
+        print(f"long K M={M} N={N} K={K} config {cfg} {info['kernel_name']} splits {info['splits']}", flush=True)
+        seen.append(cfg)
+        assert torch.equal(gemm(Wp, x, scales), want), cfg
+    monkeypatch.delenv("W4A16_PREFILL")
+    assert {10, 14, 17}.issubset(seen) and len(seen) >= 12, seen
+    for v in (1, 2, 3):
+        assert torch.equal(gemm(Wp, x, scales, variant=v), want), v
+    assert torch.equal(gemm(Wp, x, scales), want)
+    for m in sorted({17, M // 2 + 1, M - 1}):
+        if 17 <= m < M:
+            assert torch.equal(gemm(Wp, x[:m].contiguous(), scales), want[:m]), m

@@ -84,6 +84,23 @@ def test_noalloc_matches_launch_two_calls():
     assert torch.equal(y2_na, gemm(Wp, x2, scales))
 
 
+def test_noalloc_long_k_prefill_split_by_segment():
+    """A long-K prefill plan that runs one K segment per workgroup (fp32 partials and counters
+    in the scratch), twice in a row, the second smaller: equal to w4a16_launch bit for bit."""
+    torch = torch_cuda()
+    L = _lib()
+    G = 128
+    x, q, scales, Wp, key = make_problem(48, 1024, 14336, G, seed=53)
+    for m in (48, 20):
+        print(f"noalloc prefill split: M={m} N=1024 K=14336", flush=True)
+        xm = x[:m].contiguous()
+        y_na, y, plan = _both(L, torch, Wp, xm, scales, G)
+        assert plan.kernel >= 1 and plan.splits == 4 and plan.workspace_bytes == 4 * m * 1024 * 4, plan.splits
+        assert torch.equal(y_na, y)
+        assert torch.equal(y_na, gemm(Wp, xm, scales))
+        assert_close(y_na, ref_gemm(xm, q, scales, G, key))
+
+
 def test_noalloc_prefill_and_unsplit_decode():
     """Plans without a workspace run through the same entry point unchanged."""
     torch = torch_cuda()

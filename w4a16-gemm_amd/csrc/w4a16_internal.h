@@ -66,13 +66,42 @@ constexpr int prefill_lds_bytes(int cfg) {
                      (2048 * kPrefillTable[cfg].waves_n + kPrefillTable[cfg].bm / 4 * 1024)   // ring slots
                : 2 * kPrefillTable[cfg].bm * kLdsRowBytes;
 }
-// Kinds 1..3 walk K two chunks at a time; kinds 2 and 3 need at least `depth` chunk pairs and
-// kind 2 covers all M in one tile.
+// Canonical prefill accumulation order.  Every prefill config sums the K range in the same
+// order, so all of them give bit-identical results and token rows are independent of M:
+//  * K <= 8192 (KC = K/64 <= 128 chunks): one fp32 MFMA chain over the chunks in order;
+//  * longer K: S = ceil(KC / 64) segments of L = 2 ceil(KC / 2S) chunks (the last one shorter),
+//    each an MFMA chain from zero, added in fp32 in segment order (total = p0, then
+//    total = total + p_s).  The split-K configs compute one segment per workgroup and the last
+//    workgroup of a tile adds the partials; the others keep a second accumulator set.
+// 8192 keeps the BASELINE prefill shape (K = 8192) on one chain, where the 128 x 256 tiles have
+// no registers for a second set; Llama-3 down projections (K = 14336) get 4 segments of 3584.
+constexpr int prefill_segment_chunks(int KC) {
+    if (KC <= 128) return KC;
+    const int s = (KC + 63) / 64;
+    return 2 * ((KC + 2 * s - 1) / (2 * s));
+}
+constexpr int prefill_segments(int KC) {
+    return KC <= 0 ? 1 : (KC + prefill_segment_chunks(KC) - 1) / prefill_segment_chunks(KC);
+}
+// Whether a kind-1 config has the registers for a second accumulator set: not the 128 x 64
+// wave tiles budgeted for two waves per SIMD (configs 5 and 21: 128 accumulators in 256 registers).
+constexpr bool prefill_wide_segmentable(int cfg) {
+    return kPrefillTable[cfg].kind == 1 &&
+           !(kPrefillTable[cfg].wpe == 2 &&
+             (kPrefillTable[cfg].bm / kPrefillTable[cfg].waves_m) * (kPrefillTable[cfg].bn / kPrefillTable[cfg].waves_n) >=
+                 128 * 64);
+}
+// Kinds 1..3 walk K two chunks at a time; kinds 2 and 3 need at least `depth` chunk pairs in
+// every segment and kind 2 covers all M in one tile; kind 1 with several segments needs the
+// registers of a second accumulator set.
 constexpr bool prefill_shape_ok(int cfg, int M, int K) {
     return kPrefillTable[cfg].kind == 0 ||
            ((K / 64) % 2 == 0 &&
-            (kPrefillTable[cfg].kind < 2 ||
-             ((kPrefillTable[cfg].kind == 3 || M <= kPrefillTable[cfg].bm) && K / 128 >= kPrefillTable[cfg].depth)));
+            (kPrefillTable[cfg].kind == 1
+                 ? (prefill_segments(K / 64) == 1 || prefill_wide_segmentable(cfg))
+                 : ((kPrefillTable[cfg].kind == 3 || M <= kPrefillTable[cfg].bm) &&
+                    (K / 64 - (prefill_segments(K / 64) - 1) * prefill_segment_chunks(K / 64)) / 2 >=
+                        kPrefillTable[cfg].depth)));
 }
 constexpr int prefill_threads(int cfg) { return 64 * kPrefillTable[cfg].waves_m * kPrefillTable[cfg].waves_n; }
 

@@ -122,6 +122,80 @@ __device__ __forceinline__ void decode_finish(f4 sum, bool have, int rb, int lan
     }
 }
 
+// Output of a prefill tile whose lanes hold TM x NB 16x16 fp32 fragments (lane (kb, li): token
+// m0 + 16 t + li, channels 16 (nb0 + b) + 4 kb .. + 3).  One K segment per workgroup
+// (splits > 1, the canonical segments of prefill_segment_chunks): the fragments go to
+// ws[seg][m][n] (agent-scope atomic stores, as in decode_finish), and the last of the `splits`
+// workgroups of the tile adds the partials of every segment in segment order (total = p0, then
+// total + p_s) and stores fp16.  splits == 1: stored directly.  Rows past M and blocks past
+// N are neither stored nor read.
+template <int TM, int NB>
+__device__ __forceinline__ void prefill_tile_out(const f4 (&acc)[TM][NB], int m0, int nb0, int lane,
+                                                 uint16_t* __restrict__ y, float* __restrict__ ws,
+                                                 int* __restrict__ counters, int M, int N, int seg, int splits,
+                                                 int tile) {
+    const int kb = lane >> 4;
+    const int li = lane & 15;
+    const int NBLK = N >> 4;
+    if (splits == 1) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (nb0 + b >= NBLK) break;
+#pragma unroll
+            for (int t = 0; t < TM; ++t) {
+                const int m = m0 + 16 * t + li;
+                if (m < M) *reinterpret_cast<u2*>(y + (size_t)m * N + (nb0 + b) * 16 + 4 * kb) = pack_f16x4(acc[t][b]);
+            }
+        }
+        return;
+    }
+    __shared__ int s_last;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if (nb0 + b >= NBLK) break;
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            const int m = m0 + 16 * t + li;
+            if (m >= M) continue;
+            unsigned long long* q =
+                reinterpret_cast<unsigned long long*>(ws + ((size_t)seg * M + m) * N + (nb0 + b) * 16 + 4 * kb);
+            const u4 bits = __builtin_bit_cast(u4, acc[t][b]);
+            __hip_atomic_store(q, (unsigned long long)bits.x | ((unsigned long long)bits.y << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(q + 1, (unsigned long long)bits.z | ((unsigned long long)bits.w << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __builtin_amdgcn_atomic_inc32(reinterpret_cast<unsigned*>(&counters[tile]), (unsigned)(splits - 1),
+                                               __ATOMIC_RELAXED, "agent") == (unsigned)(splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+    const size_t sstride = (size_t)M * N / 2;                // one segment, in 8-byte words
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if (nb0 + b >= NBLK) break;
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            const int m = m0 + 16 * t + li;
+            if (m >= M) continue;
+            const unsigned long long* q =
+                reinterpret_cast<const unsigned long long*>(ws + (size_t)m * N + (nb0 + b) * 16 + 4 * kb);
+            f4 tot = {0.f, 0.f, 0.f, 0.f};
+            for (int sg = 0; sg < splits; ++sg) {
+                const unsigned long long lo = __hip_atomic_load(q + sg * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const unsigned long long hi = __hip_atomic_load(q + sg * sstride + 1, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT);
+                const f4 v = __builtin_bit_cast(f4, u4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)});
+                tot = sg == 0 ? v : tot + v;
+            }
+            *reinterpret_cast<u2*>(y + (size_t)m * N + (nb0 + b) * 16 + 4 * kb) = pack_f16x4(tot);
+        }
+    }
+}
+
 template <int NBW, int WAVES, int D>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
@@ -585,11 +659,11 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 // Every accumulator receives the same MFMA sequence (chunk 0 h 0, chunk 0 h 1, chunk 1 h 0,
 // ...) whatever the tile config, so all configs give bit-identical output, and token rows
 // never mix (rows past M are zero-filled and not stored).
-template <int BM, int BN, int WAVES_M, int WAVES_N>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool SEG>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64)
 prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-               int M, int N, int K, int gshift, int tiles_m) {
+               int M, int N, int K, int gshift, int tiles_m, int seg_chunks) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M;
     constexpr int WN = BN / WAVES_N;
@@ -667,6 +741,12 @@ prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
         for (int b = 0; b < TN; ++b) acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
 
+    // SEG (K split into the canonical segments of seg_chunks chunks): acc holds the running
+    // segment, total the sum of the finished ones (total = p0, then total + p_s).
+    f4 total[SEG ? TM : 1][SEG ? TN : 1];
+    int seg_left = seg_chunks;
+    bool first_seg = true;
+
     const Dq d = dq_setup(lane);
     load_x(0);
     load_w(0);
@@ -697,6 +777,19 @@ prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
                 for (int b = 0; b < TN; ++b) acc[t][b] = mfma16x16x32(a[b][h], bf, acc[t][b]);
             }
+        if constexpr (SEG) {
+            if (--seg_left == 0 || !more) {
+#pragma unroll
+                for (int t = 0; t < TM; ++t)
+#pragma unroll
+                    for (int b = 0; b < TN; ++b) {
+                        total[t][b] = first_seg ? acc[t][b] : total[t][b] + acc[t][b];
+                        acc[t][b] = f4{0.f, 0.f, 0.f, 0.f};
+                    }
+                first_seg = false;
+                seg_left = seg_chunks;
+            }
+        }
         if (more) store_x((kc + 1) & 1);
         __syncthreads();
     }
@@ -709,7 +802,7 @@ prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         for (int b = 0; b < TN; ++b) {
             if (!nb_ok[b]) continue;
             const int n = (nb0 + b) * 16 + 4 * kb;
-            *reinterpret_cast<u2*>(y + (size_t)m * N + n) = pack_f16x4(acc[t][b]);
+            *reinterpret_cast<u2*>(y + (size_t)m * N + n) = pack_f16x4(SEG ? total[SEG ? t : 0][SEG ? b : 0] : acc[t][b]);
         }
     }
 }
@@ -730,7 +823,8 @@ template <int TM, int D>
 __global__ void __launch_bounds__(64)
 prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                       const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                      int M, int N, int K, int gshift) {
+                      int M, int N, int K, int gshift, float* __restrict__ ws, int* __restrict__ counters,
+                      int splits, int seg_pairs) {
     constexpr int S = D + 1;                                 // ring slots
     constexpr int XD = 4 * TM;                               // x loads per pair (4 rows each)
     constexpr int SLOT = 1024 + XD * 1024 + 1024;            // weights, 16*TM rows x 256 B, scales
@@ -742,9 +836,12 @@ prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int lane = threadIdx.x;
     const int kb = lane >> 4;
     const int li = lane & 15;
-    const int nb = blockIdx.x;
+    const int NBLK = N >> 4;
+    const int seg = blockIdx.x / NBLK;                       // K segment (split-K over segments)
+    const int nb = blockIdx.x - seg * NBLK;
     const int KC = K >> 6;
-    const int npair = KC >> 1;
+    const int pair0 = seg * seg_pairs;
+    const int npair = min(seg_pairs, (KC >> 1) - pair0);
     const uint32_t lds = (uint32_t)reinterpret_cast<uintptr_t>(wl);
 
     // Weights: lane j fills segment j & 31 of chunk j >> 5 with packed lane 4*(seg % 8) + seg / 8.
@@ -828,12 +925,12 @@ prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // Prologue: pairs 0..D-1 (npair >= D, checked by the planner).  Steady state: wait for pair
     // p, refill with pair p + D, then compute pair p.  Drain: the last D pairs.
 #pragma unroll
-    for (int s = 0; s < D; ++s) issue(s, s);
+    for (int s = 0; s < D; ++s) issue(pair0 + s, s);
     int sc = 0, si = D;
     int p = 0;
     for (; p + D < npair; ++p) {
         wait_vmcnt<(D - 1) * OPS>();
-        issue(p + D, si);
+        issue(pair0 + p + D, si);
         consume(sc);
         sc = sc + 1 == S ? 0 : sc + 1;
         si = si + 1 == S ? 0 : si + 1;
@@ -844,11 +941,10 @@ prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         sc = sc + 1 == S ? 0 : sc + 1;
     });
 
+    f4 out[TM][1];
 #pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        const int m = 16 * t + li;
-        if (m < M) *reinterpret_cast<u2*>(y + (size_t)m * N + nb * 16 + 4 * kb) = pack_f16x4(acc[t]);
-    }
+    for (int t = 0; t < TM; ++t) out[t][0] = acc[t];
+    prefill_tile_out<TM, 1>(out, 0, nb, lane, y, ws, counters, M, N, seg, splits, nb);
 }
 
 // Prefill for token groups (any M): W waves per workgroup, NB n16 blocks per wave, share the x
@@ -876,7 +972,8 @@ template <int TM, int D, int W, int NB>
 __global__ void __launch_bounds__(64 * W)
 prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                      const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                     int M, int N, int K, int gshift, int groups_m) {
+                     int M, int N, int K, int gshift, int groups_m, float* __restrict__ ws,
+                     int* __restrict__ counters, int splits, int seg_pairs) {
     constexpr int S = D + 1;                                 // ring slots
     constexpr int XD = 4 * TM;                               // x loads per pair (4 rows each)
     constexpr int XW = XD / W;                               // x loads per wave and pair
@@ -895,19 +992,23 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kb = lane >> 4;
     const int li = lane & 15;
-    // Workgroup -> (column group, token group); consecutive blocks of one XCD (b % 8) share the
-    // column group's weights in that XCD's L2.
+    // Workgroup -> (K segment, column group, token group); consecutive blocks of one XCD (b % 8)
+    // share the column group's weights in that XCD's L2, and the segment varies slowest.
     const int G = gridDim.x;
     const int G8 = G >> 3;
     const int bid = blockIdx.x;
-    const int tile = bid < (G8 << 3) ? (bid & 7) * G8 + (bid >> 3) : bid;
+    const int tile_raw = bid < (G8 << 3) ? (bid & 7) * G8 + (bid >> 3) : bid;
+    const int tiles = G / splits;
+    const int seg = tile_raw / tiles;
+    const int tile = tile_raw - seg * tiles;
     const int tg = tile % groups_m;
     const int ng = tile / groups_m;
     const int NBLK = N >> 4;
     const int nb0_raw = (ng * W + wave) * NB;                // first n16 block of the wave
     const int m0 = tg * 16 * TM;
     const int KC = K >> 6;
-    const int npair = KC >> 1;
+    const int pair0 = seg * seg_pairs;                       // this workgroup's K segment
+    const int npair = min(seg_pairs, (KC >> 1) - pair0);
     const uint32_t lds = (uint32_t)reinterpret_cast<uintptr_t>(wl);
 
     // Weights of block b: lane j fills segment j & 31 of chunk j >> 5 with packed lane
@@ -1033,7 +1134,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // pair p (a completed direct-to-LDS load is in LDS) and consume() ends with lgkmcnt(0), which
     // is all the ordering the ring needs; __syncthreads() would also wait for vmcnt(0), draining
     // the loads of the next D pairs at every step.
-    static_for<0, D>([&](auto s) { issue(s, s); });
+    static_for<0, D>([&](auto s) { issue(pair0 + decltype(s)::value, s); });
     const int nsteady = npair - D;
     int p = 0;
     for (; p + S <= nsteady; p += S) {
@@ -1041,7 +1142,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             constexpr int T = decltype(t)::value;
             wait_vmcnt<(D - 1) * OPS>();
             __builtin_amdgcn_s_barrier();
-            issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
+            issue(pair0 + p + T + D, std::integral_constant<int, (T + D) % S>{});
             consume(t);
         });
     }
@@ -1051,7 +1152,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             constexpr int T = decltype(t)::value;
             wait_vmcnt<(D - 1) * OPS>();
             __builtin_amdgcn_s_barrier();
-            issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
+            issue(pair0 + p + T + D, std::integral_constant<int, (T + D) % S>{});
             consume(t);
         });
         static_for<0, D>([&](auto t) {
@@ -1062,16 +1163,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         });
     });
 
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int nb = nb0_raw + b;
-        if (nb >= NBLK) break;
-#pragma unroll
-        for (int t = 0; t < TM; ++t) {
-            const int m = m0 + 16 * t + li;
-            if (m < M) *reinterpret_cast<u2*>(y + (size_t)m * N + nb * 16 + 4 * kb) = pack_f16x4(acc[t][b]);
-        }
-    }
+    prefill_tile_out<TM, NB>(acc, m0, nb0_raw, lane, y, ws, counters, M, N, seg, splits, tile);
 }
 
 // ------------------------------------------------------------------------------------ launch
@@ -1113,21 +1205,32 @@ W4A16_PREFILL_CFG(21)
 
 template <int CFG>
 static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16_t* x,
-                                 const uint16_t* s, uint16_t* y, hipStream_t st) {
+                                 const uint16_t* s, uint16_t* y, float* ws, int* counters, hipStream_t st) {
     using C = PrefillCfg<CFG>;
     const int gshift = p.G == 128 ? 1 : 0;
     const int tiles_m = (p.M + C::BM - 1) / C::BM;
+    // Kinds 2 and 3 run one canonical K segment per workgroup (p.splits of them per tile).
+    const int seg_pairs = prefill_segment_chunks(p.K >> 6) >> 1;
+    const int splits = p.splits > 1 ? p.splits : 1;
     if constexpr (kPrefillTable[CFG].kind == 3)
         hipLaunchKernelGGL((prefill_group_kernel<C::BM / 16, kPrefillTable[CFG].depth, C::WN, C::BN / (16 * C::WN)>),
-                           dim3(p.grid), dim3(64 * C::WN), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
+                           dim3(p.grid), dim3(64 * C::WN), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m, ws,
+                           counters, splits, seg_pairs);
     else if constexpr (kPrefillTable[CFG].kind == 2)
         hipLaunchKernelGGL((prefill_stream_kernel<C::BM / 16, kPrefillTable[CFG].depth>), dim3(p.grid), dim3(64), 0, st,
-                           Wp, x, s, y, p.M, p.N, p.K, gshift);
+                           Wp, x, s, y, p.M, p.N, p.K, gshift, ws, counters, splits, seg_pairs);
     else if constexpr (kPrefillTable[CFG].kind == 1)
         return launch_prefill_wide(CFG, p, Wp, x, s, y, st);
     else
-        hipLaunchKernelGGL((prefill_kernel<C::BM, C::BN, C::WM, C::WN>), dim3(p.grid),
-                           dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m);
+    {
+        const int seg_chunks = prefill_segment_chunks(p.K >> 6);
+        if (prefill_segments(p.K >> 6) > 1)
+            hipLaunchKernelGGL((prefill_kernel<C::BM, C::BN, C::WM, C::WN, true>), dim3(p.grid),
+                               dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m, seg_chunks);
+        else
+            hipLaunchKernelGGL((prefill_kernel<C::BM, C::BN, C::WM, C::WN, false>), dim3(p.grid),
+                               dim3(C::WM * C::WN * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m, seg_chunks);
+    }
     return hipGetLastError();
 }
 
@@ -1147,7 +1250,7 @@ static int prefill_occupancy_of() {
     else if constexpr (kPrefillTable[CFG].kind == 1)
         return prefill_wide_occupancy(CFG);
     else
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<C::BM, C::BN, C::WM, C::WN>,
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<C::BM, C::BN, C::WM, C::WN, false>,
                                                          C::WM * C::WN * 64, 0);
     return e == hipSuccess ? n : -1;
 }
@@ -1288,6 +1391,19 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
     if (p.grid <= 0 || p.M <= 0 || p.N <= 0 || p.K <= 0) return W4A16_OK;   // empty output
     if (p.workspace_bytes && !workspace) return W4A16_ERR_WORKSPACE;
     if (p.counter_slots && !counters) return W4A16_ERR_WORKSPACE;
+    if (p.kernel >= 1 && p.kernel <= kNumPrefillTable) {
+        // A prefill plan must match what its kernel derives from the shape: the grid (tiles x
+        // K segments of the split-K kinds) bounds every segment and tile index it touches.
+        const PrefillTile& t = kPrefillTable[p.kernel];
+        const int segs = t.kind >= 2 ? prefill_segments(p.K >> 6) : 1;
+        const int64_t tiles = ((int64_t)(p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
+        if (!prefill_shape_ok(p.kernel, p.M, p.K) || (p.splits > 1 ? p.splits : 1) != segs ||
+            (int64_t)p.grid != tiles * segs)
+            return W4A16_ERR_INVALID;
+        if (segs > 1 && ((int64_t)p.counter_slots < tiles ||
+                         p.workspace_bytes < (uint64_t)segs * p.M * p.N * sizeof(float)))
+            return W4A16_ERR_WORKSPACE;
+    }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const u4* wp = reinterpret_cast<const u4*>(Wp);
     hipError_t e = hipSuccess;
@@ -1297,27 +1413,27 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
         e = launch_decode(p, wp, x, scales, y, ws, cnt, st);
     } else {
         switch (p.kernel) {
-            case 1: e = launch_prefill<1>(p, wp, x, scales, y, st); break;
-            case 2: e = launch_prefill<2>(p, wp, x, scales, y, st); break;
-            case 3: e = launch_prefill<3>(p, wp, x, scales, y, st); break;
-            case 4: e = launch_prefill<4>(p, wp, x, scales, y, st); break;
-            case 5: e = launch_prefill<5>(p, wp, x, scales, y, st); break;
-            case 6: e = launch_prefill<6>(p, wp, x, scales, y, st); break;
-            case 7: e = launch_prefill<7>(p, wp, x, scales, y, st); break;
-            case 8: e = launch_prefill<8>(p, wp, x, scales, y, st); break;
-            case 9: e = launch_prefill<9>(p, wp, x, scales, y, st); break;
-            case 10: e = launch_prefill<10>(p, wp, x, scales, y, st); break;
-            case 11: e = launch_prefill<11>(p, wp, x, scales, y, st); break;
-            case 12: e = launch_prefill<12>(p, wp, x, scales, y, st); break;
-            case 13: e = launch_prefill<13>(p, wp, x, scales, y, st); break;
-            case 14: e = launch_prefill<14>(p, wp, x, scales, y, st); break;
-            case 15: e = launch_prefill<15>(p, wp, x, scales, y, st); break;
-            case 16: e = launch_prefill<16>(p, wp, x, scales, y, st); break;
-            case 17: e = launch_prefill<17>(p, wp, x, scales, y, st); break;
-            case 18: e = launch_prefill<18>(p, wp, x, scales, y, st); break;
-            case 19: e = launch_prefill<19>(p, wp, x, scales, y, st); break;
-            case 20: e = launch_prefill<20>(p, wp, x, scales, y, st); break;
-            case 21: e = launch_prefill<21>(p, wp, x, scales, y, st); break;
+            case 1: e = launch_prefill<1>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 2: e = launch_prefill<2>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 3: e = launch_prefill<3>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 4: e = launch_prefill<4>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 5: e = launch_prefill<5>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 6: e = launch_prefill<6>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 7: e = launch_prefill<7>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 8: e = launch_prefill<8>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 9: e = launch_prefill<9>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 10: e = launch_prefill<10>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 11: e = launch_prefill<11>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 12: e = launch_prefill<12>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 13: e = launch_prefill<13>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 14: e = launch_prefill<14>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 15: e = launch_prefill<15>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 16: e = launch_prefill<16>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 17: e = launch_prefill<17>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 18: e = launch_prefill<18>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 19: e = launch_prefill<19>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 20: e = launch_prefill<20>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 21: e = launch_prefill<21>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }

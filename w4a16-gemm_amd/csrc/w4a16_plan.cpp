@@ -94,6 +94,30 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //    blocks) are at most 12 per CU: e.g. N = 28672, M = 32: 25.6 vs 49 us;
     //  * token groups of 64 rows while those waves are at most 8 per CU;
     //  * else the 128 x 128 wide tiles.
+    // Long K (several canonical segments): the token-group configs run one segment per workgroup,
+    // so their waves multiply by the segment count and larger token groups pay off sooner, and the
+    // 128 x 256 tiles are out (no registers for the second accumulator set).  Measured on the
+    // down projections (K = 14336, 28672) and K = 12288, M = 17..2048, every choice within 6% of
+    // the fastest forced config: e.g. K = 14336, N = 4096, M = 32: 19.2 us (42.8 us before the
+    // segments), M = 64: 25.9 (groups of 32, one block per wave), M = 128: 38.8 (groups of 32,
+    // two blocks per wave), M = 256: 58.1 (groups of 64), M = 512: 94.6 (64 x 128 wide tiles).
+    const int segs = prefill_segments(K / 64);
+    if (segs > 1) {
+        auto group_waves = [&](int cfg) {
+            const PrefillTile& t = kPrefillTable[cfg];
+            return std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn) * t.waves_n * segs;
+        };
+        auto group_ok = [&](int cfg) { return prefill_occupancy(cfg, lim) > 0 && prefill_shape_ok(cfg, M, K); };
+        if (M >= 1024 && wide_tiles(20) >= 0.75 * cus) return 20;
+        if (M >= 384 && wide_tiles(19) >= 0.75 * cus) return 19;
+        if (M >= 256 && wide_tiles(18) >= 0.75 * cus) return 18;
+        if (group_ok(17) && group_waves(17) <= 9.0 * cus) return 17;
+        if (M >= 128 && group_ok(13) && group_waves(12) >= 13.0 * cus) return 13;
+        if (group_ok(12) && group_waves(12) >= 5.0 * cus) return 12;
+        if (group_ok(10) && group_waves(10) <= 8.0 * cus) return 10;
+        if (wide_tiles(20) >= 0.75 * cus) return 20;
+        if (group_ok(12)) return 12;
+    }
     if (M >= 256 && M <= 2048) {
         const double t = wide_tiles(21);
         if (t >= 0.75 * cus && t <= 2.0 * cus) return 21;
@@ -295,13 +319,26 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
         if (!(cfg >= 1 && cfg <= kNumPrefillTable && prefill_occupancy(cfg, *lim) > 0))
             return fail(W4A16_ERR_NO_CONFIG, err, errlen,
                         "no prefill configuration fits (shared memory limit %d B, M=%d)", lim->lds_bytes_per_block, M);
-        const PrefillTile& t = kPrefillTable[cfg];
-        const int64_t tiles = ((int64_t)(M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
-        if (tiles > std::numeric_limits<int32_t>::max())
+        // Kinds 2 and 3 run one canonical K segment per workgroup: with several segments their
+        // tiles need a split-K counter each, else the forced variant 4 (segments in-kernel).
+        const int KC = K / 64;
+        const int segs = prefill_segments(KC);
+        auto tiles_of = [&](int c) {
+            const PrefillTile& t = kPrefillTable[c];
+            return ((int64_t)(M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+        };
+        if (kPrefillTable[cfg].kind >= 2 && segs > 1 && tiles_of(cfg) > kMaxCounterSlots) cfg = 4;
+        const int64_t tiles = tiles_of(cfg);
+        const int splits = kPrefillTable[cfg].kind >= 2 ? segs : 1;
+        if (tiles * splits > std::numeric_limits<int32_t>::max())
             return fail(W4A16_ERR_INVALID, err, errlen, "M too large for prefill config %d", cfg);
         out.kernel = cfg;
         out.block = prefill_threads(cfg);
-        out.grid = (int32_t)tiles;
+        out.grid = (int32_t)(tiles * splits);
+        out.splits = splits;
+        out.slab_chunks = prefill_segment_chunks(KC);
+        out.counter_slots = splits > 1 ? (int32_t)tiles : 0;
+        out.workspace_bytes = splits > 1 ? (uint64_t)splits * M * N * sizeof(float) : 0;
         if (debug_enabled())
             std::fprintf(stderr, "prefill dispatch G=%d M=%d N=%d K=%d cfg=%d occ=%d tiles=%d\n",
                          G, M, N, K, cfg, prefill_occupancy(cfg, *lim), out.grid);

@@ -56,11 +56,14 @@ namespace w4a16 {
 // (1 x 2) stay at 1: at 2, 256 x 128 spills 67 times inside its loop and 128 x 128 spills a
 // pending asm-load destination (tests/test_isa_hazards.py rejects that).  The 32-channel wave
 // tiles (configs 18..20) and the 8-wave 256 x 256 tile fit 2 without spills.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE>
+// SEG: K longer than one canonical segment (seg_chunks chunks, even): acc holds the running
+// segment and total the sum of the finished ones (total = p0, then total + p_s), closed after
+// every seg_chunks chunks of the two-chunk loop.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE, bool SEG>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                    int M, int N, int K, int gshift, int tiles_m, int group_m) {
+                    int M, int N, int K, int gshift, int tiles_m, int group_m, int seg_chunks) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M;
     constexpr int WN = BN / WAVES_N;
@@ -172,6 +175,10 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[p][q][i] = 0.f;
 
+    f32x16 total[SEG ? TM : 1][SEG ? TN : 1];
+    int seg_left = seg_chunks;
+    bool first_seg = true;
+
     const Dq d = dq_setup(r);                                  // nibble parity of channel r % 16
     const uint32_t xrow = (uint32_t)reinterpret_cast<uintptr_t>(xs) + (wm * WM + r) * kXRow + kg * 16;
     // One chunk: for each half h, the 2 TM B operands are read from LDS through asm (the compiler
@@ -240,6 +247,21 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         compute(1, w1, s1);
         load_w(kc + 3, w1, s1);
         __syncthreads();
+        if constexpr (SEG) {
+            seg_left -= 2;
+            if (seg_left == 0 || kc + 2 >= KC) {
+#pragma unroll
+                for (int p = 0; p < TM; ++p)
+#pragma unroll
+                    for (int q = 0; q < TN; ++q) {
+                        total[p][q] = first_seg ? acc[p][q] : total[p][q] + acc[p][q];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) acc[p][q][i] = 0.f;
+                    }
+                first_seg = false;
+                seg_left = seg_chunks;
+            }
+        }
     }
     // No load in flight at exit.  The registers of the last (unused) prefetches are re-bound
     // after the wait: otherwise the compiler, seeing them dead, reuses them before it.
@@ -270,7 +292,9 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                 const int n = (nb0 + 2 * q) * 16 + 8 * g + 4 * kg_e;
                 if (nbk < NBLK)
                     *reinterpret_cast<u2*>(y + (size_t)m * N + n) =
-                        pack_f16x4(f4{acc[p][q][4 * g], acc[p][q][4 * g + 1], acc[p][q][4 * g + 2], acc[p][q][4 * g + 3]});
+                        pack_f16x4(SEG ? f4{total[SEG ? p : 0][SEG ? q : 0][4 * g], total[SEG ? p : 0][SEG ? q : 0][4 * g + 1],
+                                            total[SEG ? p : 0][SEG ? q : 0][4 * g + 2], total[SEG ? p : 0][SEG ? q : 0][4 * g + 3]}
+                                       : f4{acc[p][q][4 * g], acc[p][q][4 * g + 1], acc[p][q][4 * g + 2], acc[p][q][4 * g + 3]});
             }
         }
     }
@@ -290,9 +314,20 @@ static hipError_t launch_wide(const w4a16_plan& p, const u4* Wp, const uint16_t*
         const int g = std::atoi(o);
         if (g >= 1) group_m = std::min(g, tiles_m);
     }
-    hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe>), dim3(p.grid),
-                       dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
-                       group_m);
+    const int KC = p.K >> 6;
+    const int seg_chunks = prefill_segment_chunks(KC);
+    if (prefill_segments(KC) > 1) {
+        if constexpr (prefill_wide_segmentable(CFG))
+            hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, true>), dim3(p.grid),
+                               dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
+                               group_m, seg_chunks);
+        else
+            return hipErrorInvalidValue;                      // no registers for a second set (planner never asks)
+    } else {
+        hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false>), dim3(p.grid),
+                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
+                           group_m, seg_chunks);
+    }
     return hipGetLastError();
 }
 
@@ -316,7 +351,7 @@ template <int CFG>
 static int occupancy_wide() {
     constexpr PrefillTile c = kPrefillTable[CFG];
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false>,
                                                      c.waves_m * c.waves_n * 64, 0) != hipSuccess)
         return -1;
     return n;

@@ -24,7 +24,8 @@
 
 namespace {
 
-// Decode split-K counters.  Launches that share a counter buffer must not overlap in time
+// Split-K counters (decode split-K and the long-K prefill token-group configs, which run one
+// K segment per workgroup).  Launches that share a counter buffer must not overlap in time
 // (w4a16.h), and work on different streams may overlap, so:
 //  * eager calls keep one buffer per (device, stream): zeroed when created, left zero by every
 //    launch;
@@ -61,7 +62,7 @@ void ensure_capture_pool(const at::Tensor& like) {
         g_capture_pool[dev].buf = torch::zeros({kCapturePoolSlots}, like.options().dtype(torch::kInt32));
 }
 
-at::Tensor decode_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
+at::Tensor split_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
     const auto opts = like.options().dtype(torch::kInt32);
     const int dev = (int)like.device().index();
     std::lock_guard<std::mutex> lk(g_mu);
@@ -133,7 +134,7 @@ torch::Tensor w4a16_gemm(torch::Tensor Wp, torch::Tensor x, torch::Tensor scales
     torch::Tensor cnt_t;
     int32_t* cnt = nullptr;
     if (plan.counter_slots) {
-        cnt_t = decode_counters(x, stream, plan.counter_slots);
+        cnt_t = split_counters(x, stream, plan.counter_slots);
         cnt = cnt_t.data_ptr<int32_t>();
     }
 

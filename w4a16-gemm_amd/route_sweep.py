@@ -59,6 +59,7 @@ def main(argv=None) -> int:
     ap.add_argument("--target-mb", type=float, default=512)
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--md", default=None, help="write the summary table (Markdown) here")
+    ap.add_argument("--json", default=None, help="write every timing (auto and each forced setting) here")
     args = ap.parse_args(argv)
     Ms = [int(v) for v in args.M.split(",")]
     shapes = SHAPES if not args.shape else [
@@ -70,7 +71,7 @@ def main(argv=None) -> int:
     for var in ("W4A16_PREFILL", "W4A16_DECODE"):
         os.environ.pop(var, None)
 
-    rows = []
+    rows, dump = [], []
     for index, (name, N, K, G) in enumerate(shapes):
         weights, _ = load_weights(torch, N, K, G, args.target_mb, seed=index)
         for M in Ms:
@@ -98,6 +99,8 @@ def main(argv=None) -> int:
             auto_us = times["auto"]
             best = min(((label, times[label], kname) for label, _, _, kname in forced), key=lambda b: b[1])
             rows.append((name, N, K, G, M, auto["kernel_name"], auto_us, best))
+            dump.append({"shape": name, "N": N, "K": K, "G": G, "M": M, "auto": auto["kernel_name"],
+                         "times_us": times, "kernels": {label: kname for label, _, _, kname in forced}})
             print(f"{name} N={N} K={K} G={G} M={M}: auto {auto['kernel_name']} {auto_us:.2f} us; "
                   f"best forced {best[0]} {best[2]} {best[1]:.2f} us; auto/best {auto_us / best[1]:.3f}", flush=True)
             del x, calls
@@ -115,6 +118,10 @@ def main(argv=None) -> int:
     if args.md:
         with open(args.md, "w", encoding="utf-8") as f:
             f.write(table + "\n")
+    if args.json:
+        import json
+        with open(args.json, "w", encoding="utf-8") as f:
+            json.dump(dump, f, indent=1)
     worst = max(aus / bus for *_, aus, (_, bus, _) in rows)
     print(f"worst auto/best ratio: {worst:.3f}; rows over 1.05: {sum(aus > 1.05 * bus for *_, aus, (_, bus, _) in rows)}")
     return 0
