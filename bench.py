@@ -486,6 +486,9 @@ def main(argv=None) -> int:
                          "kernel (64 MiB elementwise copy), no benchmark line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
+    ap.add_argument("--no-c1", action="store_true",
+                    help="skip the configs[0] decode leg (for counter runs of the headline calls: its kernel has "
+                         "the name of the down M=1 kernel)")
     ap.add_argument("--json", default=None, help="also write the JSON line to this file")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -574,7 +577,7 @@ def main(argv=None) -> int:
         pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
                             a.warmup if a.workload == "prefill" else 3)
     mod = bench_moderate(torch, gemm, 30, 3) if (dec is not None and not a.no_prefill) else None
-    c1 = bench_c1(torch, gemm, 40, 3) if dec is not None else None
+    c1 = bench_c1(torch, gemm, 40, 3) if (dec is not None and not a.no_c1) else None
     gv = bench_gemv(torch, 20, 3) if (dec is not None and not a.no_prefill) else None
 
     out = {"metric": "decode GB/s & %HBM peak (M=1..16); prefill TFLOP/s & %MFMA peak (M=2048)"}
@@ -623,6 +626,7 @@ def main(argv=None) -> int:
                          "frac_mfma": round(mod["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
                          "frac_hbm": round(mod["GBs"] / HBM_PEAK_GBS, 4),
                          "flops_per_launch": alg_flops(M, N, K), "bytes_per_launch": alg_bytes(M, N, K, Gm)}}
+        tag_counters(out["moderate"]["roofline"], "moderate", [mod["kernel"]], ["traffic", "mfma_busy_frac", "clock_ghz"])
     if c1 is not None:
         _, N, K, M = C1_CASE
         out["decode_c1"] = {

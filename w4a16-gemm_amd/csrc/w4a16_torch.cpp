@@ -185,10 +185,11 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
     d["decode_variant"] = plan.decode_variant;
     // Names as the compiler demangles them (what rocprofv3 reports), e.g.
     // "w4a16::decode_ring_kernel<2, 4, 2, 1>".
-    auto tmpl = [](const char* name, std::initializer_list<int> args) {
+    auto tmpl = [](const char* name, std::initializer_list<int> args, const char* last = nullptr) {
         std::string s = std::string("w4a16::") + name + "<";
         bool first = true;
         for (int a : args) { s += (first ? "" : ", ") + std::to_string(a); first = false; }
+        if (last) s += std::string(", ") + last;
         return s + ">";
     };
     if (plan.kernel == W4A16_VARIANT_DECODE) {
@@ -202,10 +203,14 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
             d["kernel_name"] = tmpl("prefill_stream_kernel", {t.bm / 16, t.depth});
         else if (t.kind == 3)
             d["kernel_name"] = tmpl("prefill_group_kernel", {t.bm / 16, t.depth, t.waves_n, t.bn / (16 * t.waves_n)});
-        else if (t.kind == 1)
-            d["kernel_name"] = tmpl("prefill_wide_kernel", {t.bm, t.bn, t.waves_m, t.waves_n, t.wpe});
-        else
-            d["kernel_name"] = tmpl("prefill_kernel", {t.bm, t.bn, t.waves_m, t.waves_n});
+        else {
+            // the wide and tiled kernels carry the long-K segment flag as their last template argument
+            const char* seg = w4a16::prefill_segments((int)(K / 64)) > 1 ? "true" : "false";
+            if (t.kind == 1)
+                d["kernel_name"] = tmpl("prefill_wide_kernel", {t.bm, t.bn, t.waves_m, t.waves_n, t.wpe}, seg);
+            else
+                d["kernel_name"] = tmpl("prefill_kernel", {t.bm, t.bn, t.waves_m, t.waves_n}, seg);
+        }
     }
     d["cu_count"] = lim.cu_count; d["gcn_arch"] = lim.gcn_arch; d["lds_bytes_per_block"] = lim.lds_bytes_per_block;
     return d;
