@@ -244,13 +244,15 @@ def test_wide_prefill_accumulators_stay_in_place(isa):
     for name, lines in ks.items():
         if "Lb1E" in name:
             continue
-        bm, bn, wm, wn, _ = (int(v) for v in re.search(r"ILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb0EE", name).groups())
+        bm, bn, wm, wn, _, depth = (int(v) for v in
+                                    re.search(r"ILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb0ELi(\d+)EE", name).groups())
         tm, tn = bm // wm // 32, bn // wn // 32
         loops = [l for l in _loop_bodies(lines) if any("v_mfma" in t for t in l)]
         assert len(loops) == 1, (name, len(loops))
         ops = [t.split()[0] for t in loops[0]]
-        # two chunks of a (32 tm) x (32 tn) wave tile = 16 tm tn 16x16x32 MFMAs' work (a 32x32x16 counts twice)
+        # `depth` chunks per loop iteration; one chunk of a (32 tm) x (32 tn) wave tile = 8 tm tn
+        # 16x16x32 MFMAs' work (a 32x32x16 counts twice)
         work = ops.count("v_mfma_f32_16x16x32_f16") + 2 * ops.count("v_mfma_f32_32x32x16_f16")
-        assert work == 16 * tm * tn, (name, work)
+        assert work == 8 * tm * tn * depth, (name, work)
         moves = [o for o in ops if o.startswith("v_accvgpr")]
         assert not moves, (name, len(moves))

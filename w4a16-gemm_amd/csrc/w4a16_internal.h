@@ -13,6 +13,8 @@ namespace w4a16 {
 // 10..17 run prefill_group_kernel (kind 3: waves_n waves, one or more n16 blocks each, share the
 // x rows of a group of bm tokens in the ring; any M, one token group per grid row).  The auto
 // planner (or the W4A16_PREFILL override) picks among all of them; all give bit-identical output.
+//   depth: kinds 2 and 3: chunk pairs in flight in the ring; kind 1: register sets of prefetched
+//          chunks (2 or 4: loads issued that many chunks ahead; K/64 must be a multiple);
 //   wpe: waves per SIMD the kind-1 kernels' registers are budgeted for (amdgpu_waves_per_eu);
 //   occ: resident workgroups per CU of the compiled kernel on gfx950 (registers, LDS and wave
 //        slots), the value hipOccupancyMaxActiveBlocksPerMultiprocessor reports for it
@@ -26,9 +28,9 @@ constexpr PrefillTile kPrefillTable[22] = {
     {32, 128, 1, 4, 0, 0, 0, 6},     // 2: wave tile 32 x 32
     {64, 128, 2, 2, 0, 0, 0, 3},     // 3: wave tile 32 x 64
     {128, 128, 2, 2, 0, 0, 0, 2},    // 4: wave tile 64 x 64
-    {128, 256, 1, 4, 1, 0, 2, 2},    // 5: wave tile 128 x 64, 4 waves across N
-    {256, 128, 2, 2, 1, 0, 1, 1},    // 6: wave tile 128 x 64, 2 x 2 waves
-    {128, 128, 1, 2, 1, 0, 1, 2},    // 7: wave tile 128 x 64, 2 waves
+    {128, 256, 1, 4, 1, 2, 2, 2},    // 5: wave tile 128 x 64, 4 waves across N
+    {256, 128, 2, 2, 1, 2, 1, 1},    // 6: wave tile 128 x 64, 2 x 2 waves
+    {128, 128, 1, 2, 1, 2, 1, 2},    // 7: wave tile 128 x 64, 2 waves
     {32, 16, 1, 1, 2, 6, 0, 2},      // 8: M <= 32, one wave per n16 block, 6 pairs in flight
     {64, 16, 1, 1, 2, 3, 0, 2},      // 9: M <= 64, one wave per n16 block, 3 pairs in flight
     {32, 64, 1, 4, 3, 3, 0, 3},      // 10: groups of 32 tokens, 4 n16 blocks per workgroup, 3 pairs
@@ -39,10 +41,10 @@ constexpr PrefillTile kPrefillTable[22] = {
     {32, 256, 1, 4, 3, 2, 0, 2},     // 15: groups of 32 tokens, 4 n16 blocks per wave, 2 pairs (forced only)
     {16, 64, 1, 4, 3, 3, 0, 4},      // 16: groups of 16 tokens, 1 n16 block per wave, 3 pairs
     {16, 64, 1, 4, 3, 4, 0, 3},      // 17: groups of 16 tokens, 1 n16 block per wave, 4 pairs
-    {64, 128, 1, 4, 1, 0, 2, 3},     // 18: wave tile 64 x 32, 4 waves across N
-    {64, 256, 1, 8, 1, 0, 2, 2},     // 19: wave tile 64 x 32, 8 waves across N share the x rows
-    {128, 128, 1, 4, 1, 0, 2, 2},    // 20: wave tile 128 x 32, 4 waves across N
-    {256, 256, 2, 4, 1, 0, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves
+    {64, 128, 1, 4, 1, 4, 2, 3},     // 18: wave tile 64 x 32, 4 waves across N
+    {64, 256, 1, 8, 1, 2, 2, 2},     // 19: wave tile 64 x 32, 8 waves across N share the x rows
+    {128, 128, 1, 4, 1, 4, 2, 2},    // 20: wave tile 128 x 32, 4 waves across N
+    {256, 256, 2, 4, 1, 2, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
 constexpr int kNumPrefillTable = 21;     // all prefill configs
@@ -91,14 +93,28 @@ constexpr bool prefill_wide_segmentable(int cfg) {
              (kPrefillTable[cfg].bm / kPrefillTable[cfg].waves_m) * (kPrefillTable[cfg].bn / kPrefillTable[cfg].waves_n) >=
                  128 * 64);
 }
+// Chunks a kind-1 kernel walks per loop step (its register sets of prefetched chunks): `depth`,
+// except with the second accumulator set of the long-K segments on the 128 x 32 wave tiles
+// budgeted for two waves per SIMD, which then have registers for two sets only.
+constexpr int prefill_wide_steps(int cfg, bool seg) {
+    return seg && kPrefillTable[cfg].wpe == 2 &&
+                   (kPrefillTable[cfg].bm / kPrefillTable[cfg].waves_m) * (kPrefillTable[cfg].bn / kPrefillTable[cfg].waves_n) >=
+                       128 * 32
+               ? 2
+               : kPrefillTable[cfg].depth;
+}
 // Kinds 1..3 walk K two chunks at a time; kinds 2 and 3 need at least `depth` chunk pairs in
-// every segment and kind 2 covers all M in one tile; kind 1 with several segments needs the
-// registers of a second accumulator set.
+// every segment and kind 2 covers all M in one tile; kind 1 walks K `depth` chunks at a time
+// and, with several segments, needs the registers of a second accumulator set and segments of
+// a whole number of steps.
 constexpr bool prefill_shape_ok(int cfg, int M, int K) {
     return kPrefillTable[cfg].kind == 0 ||
            ((K / 64) % 2 == 0 &&
             (kPrefillTable[cfg].kind == 1
-                 ? (prefill_segments(K / 64) == 1 || prefill_wide_segmentable(cfg))
+                 ? (prefill_segments(K / 64) == 1
+                        ? (K / 64) % prefill_wide_steps(cfg, false) == 0
+                        : prefill_wide_segmentable(cfg) && (K / 64) % prefill_wide_steps(cfg, true) == 0 &&
+                              prefill_segment_chunks(K / 64) % prefill_wide_steps(cfg, true) == 0)
                  : ((kPrefillTable[cfg].kind == 3 || M <= kPrefillTable[cfg].bm) &&
                     (K / 64 - (prefill_segments(K / 64) - 1) * prefill_segment_chunks(K / 64)) / 2 >=
                         kPrefillTable[cfg].depth)));

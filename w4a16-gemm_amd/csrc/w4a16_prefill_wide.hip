@@ -59,7 +59,7 @@ namespace w4a16 {
 // SEG: K longer than one canonical segment (seg_chunks chunks, even): acc holds the running
 // segment and total the sum of the finished ones (total = p0, then total + p_s), closed after
 // every seg_chunks chunks of the two-chunk loop.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE, bool SEG>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE, bool SEG, int R>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
@@ -134,13 +134,13 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         xoff[i] = ((uint32_t)(min(m0 + (sg >> 3), M - 1) - m0) * (uint32_t)K + (sg & 7) * 8) * 2;
     }
 
-    u4 xr0[SPT], xr1[SPT];
-    auto load_x = [&](int kc, u4 (&xr)[SPT]) {
+    u4 xr[R][SPT];                                            // R register sets of prefetched chunks
+    auto load_x = [&](int kc, u4 (&xr)[SPT]) __attribute__((always_inline)) {
         const char* xb = xbase + (size_t)min(kc, KC - 1) * 128;   // past the end: harmless reload
 #pragma unroll
         for (int i = 0; i < SPT; ++i) xr[i] = gload_u4_sbase(xb, xoff[i]);
     };
-    auto store_x = [&](int buf, u4 (&xr)[SPT]) {
+    auto store_x = [&](int buf, u4 (&xr)[SPT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < SPT; ++i) bind_after_wait(xr[i]);
 #pragma unroll
@@ -149,9 +149,9 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             lds_store_xseg(xs + buf * XBUF + (sg >> 3) * kXRow, sg & 7, xr[i]);
         }
     };
-    u4 w0[TN][2], w1[TN][2];
-    uint32_t s0[TN], s1[TN];
-    auto load_w = [&](int kc, u4 (&w)[TN][2], uint32_t (&s)[TN]) {
+    u4 wr[R][TN][2];
+    uint32_t sr[R][TN];
+    auto load_w = [&](int kc, u4 (&w)[TN][2], uint32_t (&s)[TN]) __attribute__((always_inline)) {
         const int kcl = min(kc, KC - 1);
 #pragma unroll
         for (int q = 0; q < TN; ++q)
@@ -160,11 +160,13 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
         for (int q = 0; q < TN; ++q) s[q] = gload_u16_sbase(sbase[q] + (size_t)(kcl >> gshift) * N * 2, soff[q]);
     };
-    // Per chunk: SPT x loads and 3 TN weight/scale loads.  Loads younger than x of chunk c+1 when
-    // chunk c starts: weights c, x c+2, weights c+1; younger than the weights of chunk c once x of
-    // chunk c+3 is issued: x c+2, weights c+1, x c+3.
-    constexpr int WAIT_X = 6 * TN + SPT;
-    constexpr int WAIT_W = 2 * SPT + 3 * TN;
+    // Per chunk: SPT x loads and 3 TN weight/scale loads.  In flight when chunk c starts, oldest
+    // first: x c+1, weights c, x c+2, weights c+1, ..., x c+R, weights c+R-1.  Younger than x of
+    // chunk c+1: weights c and R-1 chunks' loads; younger than the weights of chunk c once x of
+    // chunk c+1+R is issued: R-1 chunks' loads and that x.
+    constexpr int WAIT_X = 3 * TN + (R - 1) * (SPT + 3 * TN);
+    constexpr int WAIT_W = (R - 1) * (SPT + 3 * TN) + SPT;
+    static_assert(R == 2 || R == 4, "register sets: the x LDS buffer parity must be static in the unrolled loop");
     static_assert(WAIT_X <= 63 && WAIT_W <= 63, "vmcnt range");
 
     f32x16 acc[TM][TN];
@@ -184,7 +186,7 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // One chunk: for each half h, the 2 TM B operands are read from LDS through asm (the compiler
     // would follow each read with a full lgkmcnt wait), the 2 TN A operands are dequantised
     // while the reads are in flight, then one wait and the 4 TM TN MFMAs (tp = 0 before tp = 1).
-    auto compute = [&](int buf, u4 (&w)[TN][2], uint32_t (&s)[TN]) {
+    auto compute = [&](int buf, u4 (&w)[TN][2], uint32_t (&s)[TN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < TN; ++q) {
             bind_after_wait(w[q][0]); bind_after_wait(w[q][1]); bind_after_wait(s[q]);
@@ -219,37 +221,37 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         }
     };
 
-    // Issue order: prologue x0 | x1 w0 x2 w1; then chunk c issues x(c+3) and w(c+2).  Chunk c
-    // uses x buffer c & 1, x register set and weight set c & 1 (the loop is unrolled by two
-    // chunks; K/64 is even, checked by the planner).  x of chunk c+1 is written to the other LDS
-    // buffer first, so those LDS writes overlap the MFMAs.  One barrier per chunk orders both
-    // buffers.  Loads past the end re-read the last chunk into registers nobody uses again.
-    load_x(0, xr0);
+    // Issue order: prologue x0 | x1 w0 x2 w1 ... x(R) w(R-1); then chunk c issues x(c+1+R) and
+    // w(c+R).  Chunk c uses x buffer c & 1, and register set c % R for its weights and for x of
+    // chunk c+1 (the loop is unrolled by R chunks; K/64 is a multiple of R, checked by the
+    // planner).  x of chunk c+1 is written to the other LDS buffer first, so those LDS writes
+    // overlap the MFMAs.  One barrier per chunk orders both buffers.  Loads past the end re-read
+    // the last chunk into registers nobody uses again.  SEG: a segment closes after every
+    // seg_chunks chunks (and at the end), a multiple of R (checked by the planner).
+    load_x(0, xr[0]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    store_x(0, xr0);
-    load_x(1, xr1);
-    load_w(0, w0, s0);
-    load_x(2, xr0);
-    load_w(1, w1, s1);
+    store_x(0, xr[0]);
+    static_for<1, R + 1>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        load_x(J, xr[J % R]);
+        load_w(J - 1, wr[(J - 1) % R], sr[(J - 1) % R]);
+    });
     __syncthreads();
-    for (int kc = 0; kc < KC; kc += 2) {
-        wait_vmcnt<WAIT_X>();
-        store_x(1, xr1);
-        load_x(kc + 3, xr1);
-        wait_vmcnt<WAIT_W>();
-        compute(0, w0, s0);
-        load_w(kc + 2, w0, s0);
-        __syncthreads();
-        wait_vmcnt<WAIT_X>();
-        store_x(0, xr0);
-        load_x(kc + 4, xr0);
-        wait_vmcnt<WAIT_W>();
-        compute(1, w1, s1);
-        load_w(kc + 3, w1, s1);
-        __syncthreads();
+    for (int kc = 0; kc < KC; kc += R) {
+        static_for<0, R>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            const int c = kc + T;
+            wait_vmcnt<WAIT_X>();
+            store_x((T + 1) & 1, xr[(T + 1) % R]);
+            load_x(c + 1 + R, xr[(T + 1) % R]);
+            wait_vmcnt<WAIT_W>();
+            compute(T & 1, wr[T], sr[T]);
+            load_w(c + R, wr[T], sr[T]);
+            __syncthreads();
+        });
         if constexpr (SEG) {
-            seg_left -= 2;
-            if (seg_left == 0 || kc + 2 >= KC) {
+            seg_left -= R;
+            if (seg_left == 0 || kc + R >= KC) {
 #pragma unroll
                 for (int p = 0; p < TM; ++p)
 #pragma unroll
@@ -267,12 +269,15 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // after the wait: otherwise the compiler, seeing them dead, reuses them before it.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < SPT; ++i) { bind_after_wait(xr0[i]); bind_after_wait(xr1[i]); }
+    for (int j = 0; j < R; ++j)
 #pragma unroll
-    for (int q = 0; q < TN; ++q) {
-        bind_after_wait(w0[q][0]); bind_after_wait(w0[q][1]); bind_after_wait(s0[q]);
-        bind_after_wait(w1[q][0]); bind_after_wait(w1[q][1]); bind_after_wait(s1[q]);
-    }
+        for (int i = 0; i < SPT; ++i) bind_after_wait(xr[j][i]);
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+            bind_after_wait(wr[j][q][0]); bind_after_wait(wr[j][q][1]); bind_after_wait(sr[j][q]);
+        }
 
     // The lane id again, from v_mbcnt (opaque to the compiler): keeping r and kg live across the
     // loop would cost two registers, which at two waves per SIMD the allocator spills.
@@ -318,13 +323,13 @@ static hipError_t launch_wide(const w4a16_plan& p, const u4* Wp, const uint16_t*
     const int seg_chunks = prefill_segment_chunks(KC);
     if (prefill_segments(KC) > 1) {
         if constexpr (prefill_wide_segmentable(CFG))
-            hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, true>), dim3(p.grid),
+            hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, true, prefill_wide_steps(CFG, true)>), dim3(p.grid),
                                dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
                                group_m, seg_chunks);
         else
             return hipErrorInvalidValue;                      // no registers for a second set (planner never asks)
     } else {
-        hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false>), dim3(p.grid),
+        hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false, prefill_wide_steps(CFG, false)>), dim3(p.grid),
                            dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
                            group_m, seg_chunks);
     }
@@ -351,7 +356,7 @@ template <int CFG>
 static int occupancy_wide() {
     constexpr PrefillTile c = kPrefillTable[CFG];
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false, prefill_wide_steps(CFG, false)>,
                                                      c.waves_m * c.waves_n * 64, 0) != hipSuccess)
         return -1;
     return n;

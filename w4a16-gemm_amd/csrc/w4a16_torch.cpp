@@ -205,9 +205,13 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
             d["kernel_name"] = tmpl("prefill_group_kernel", {t.bm / 16, t.depth, t.waves_n, t.bn / (16 * t.waves_n)});
         else {
             // the wide and tiled kernels carry the long-K segment flag as their last template argument
-            const char* seg = w4a16::prefill_segments((int)(K / 64)) > 1 ? "true" : "false";
-            if (t.kind == 1)
-                d["kernel_name"] = tmpl("prefill_wide_kernel", {t.bm, t.bn, t.waves_m, t.waves_n, t.wpe}, seg);
+            const bool segs = w4a16::prefill_segments((int)(K / 64)) > 1;
+            const char* seg = segs ? "true" : "false";
+            if (t.kind == 1) {
+                std::string n = tmpl("prefill_wide_kernel", {t.bm, t.bn, t.waves_m, t.waves_n, t.wpe}, seg);
+                d["kernel_name"] = n.substr(0, n.size() - 1) + ", " +
+                                   std::to_string(w4a16::prefill_wide_steps(plan.kernel, segs)) + ">";
+            }
             else
                 d["kernel_name"] = tmpl("prefill_kernel", {t.bm, t.bn, t.waves_m, t.waves_n}, seg);
         }
