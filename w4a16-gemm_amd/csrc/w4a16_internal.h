@@ -41,7 +41,7 @@ constexpr PrefillTile kPrefillTable[22] = {
     {32, 256, 1, 4, 3, 2, 0, 2},     // 15: groups of 32 tokens, 4 n16 blocks per wave, 2 pairs (forced only)
     {16, 64, 1, 4, 3, 3, 0, 4},      // 16: groups of 16 tokens, 1 n16 block per wave, 3 pairs
     {16, 64, 1, 4, 3, 4, 0, 3},      // 17: groups of 16 tokens, 1 n16 block per wave, 4 pairs
-    {64, 128, 1, 4, 1, 4, 2, 3},     // 18: wave tile 64 x 32, 4 waves across N
+    {64, 128, 1, 4, 1, 4, 2, 2},     // 18: wave tile 64 x 32, 4 waves across N
     {64, 256, 1, 8, 1, 2, 2, 2},     // 19: wave tile 64 x 32, 8 waves across N share the x rows
     {128, 128, 1, 4, 1, 4, 2, 2},    // 20: wave tile 128 x 32, 4 waves across N
     {256, 256, 2, 4, 1, 2, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves
