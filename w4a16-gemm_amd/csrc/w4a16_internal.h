@@ -77,9 +77,10 @@ constexpr int prefill_lds_bytes(int cfg) {
 //    workgroup of a tile adds the partials; the others keep a second accumulator set.
 // 8192 keeps the BASELINE prefill shape (K = 8192) on one chain, where the 128 x 256 tiles have
 // no registers for a second set; Llama-3 down projections (K = 14336) get 4 segments of 3584.
+constexpr int kMaxSegmentChunks = 64;       // longest canonical segment above K = 8192 (chunks of 64)
 constexpr int prefill_segment_chunks(int KC) {
     if (KC <= 128) return KC;
-    const int s = (KC + 63) / 64;
+    const int s = (KC + kMaxSegmentChunks - 1) / kMaxSegmentChunks;
     return 2 * ((KC + 2 * s - 1) / (2 * s));
 }
 constexpr int prefill_segments(int KC) {
