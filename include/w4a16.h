@@ -64,7 +64,8 @@ typedef struct w4a16_device_limits {
     int32_t cu_count;             /* compute units (256 on MI355X)                      */
     int32_t lds_bytes_per_block;  /* max LDS bytes one workgroup may allocate            */
     int32_t max_threads_per_block;
-    int32_t gcn_arch;             /* e.g. 950 for gfx950; 0 = unknown                     */
+    int32_t gcn_arch;             /* major*100 + minor*10 + stepping: 950 for gfx950,    */
+                                  /* 910 for gfx90a, 1100 for gfx1100; 0 = unknown        */
 } w4a16_device_limits;
 
 /* A launch plan: the result of validation + routing + selection.  Plain data; copyable. */

@@ -308,6 +308,18 @@ def test_planner_occupancy_hook_covers_every_prefill_config(lib):
     assert all(lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(older)) <= o for cfg, o in zip(range(1, 22), occ))
 
 
+@pytest.mark.parametrize("name,want", [
+    (b"gfx950:sramecc+:xnack-", 950), (b"gfx950", 950), (b"gfx942:sramecc+:xnack-", 942), (b"gfx90a:xnack-", 910),
+    (b"gfx1100", 1100), (b"gfx1201", 1201), (b"gfx908", 908),
+    (b"", 0), (b"sm_90", 0), (b"gfx9", 0), (b"gfx9x0", 0), (b"gfx95g", 0), (None, 0)])
+def test_gcn_arch_name_parse(lib, name, want):
+    """hipDeviceProp_t.gcnArchName -> w4a16_device_limits.gcn_arch (major*100 + minor*10 + stepping,
+    the last two characters hex digits); only 950 selects the 160 KB LDS per CU."""
+    lib.w4a16_debug_parse_gcn_arch.argtypes = [ctypes.c_char_p]
+    lib.w4a16_debug_parse_gcn_arch.restype = ctypes.c_int32
+    assert lib.w4a16_debug_parse_gcn_arch(name) == want
+
+
 @pytest.mark.parametrize("M,N,K,want", [
     (1, 14336, 4096, (20, 1)), (4, 14336, 4096, (20, 1)), (8, 14336, 4096, (16, 1)), (16, 14336, 4096, (16, 1)),
     (1, 4096, 14336, (29, 1)), (4, 4096, 14336, (29, 1)), (8, 4096, 14336, (19, 1)), (16, 4096, 14336, (20, 2)),

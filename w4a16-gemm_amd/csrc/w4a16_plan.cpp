@@ -161,6 +161,28 @@ extern "C" const char* w4a16_last_error(void) { return g_last_error.c_str(); }
 extern "C" int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
 
 // Test hook (no counterpart in the reference): the planner's occupancy for prefill config `cfg`.
+// gcn_arch of an architecture name "gfx<major><minor><stepping>[:features]": minor and stepping are
+// the last two characters before ':' (hex digits), major the decimal digits before them;
+// encoded major * 100 + minor * 10 + stepping (gfx950 -> 950, gfx942 -> 942, gfx90a -> 910,
+// gfx1100 -> 1100); 0 when the name does not parse.
+static int32_t parse_gcn_arch(const char* a) {
+    if (!a || std::strncmp(a, "gfx", 3) != 0) return 0;
+    const char* s = a + 3;
+    size_t n = std::strcspn(s, ":");
+    if (n < 3) return 0;
+    int32_t major = 0;
+    for (size_t i = 0; i + 2 < n; ++i) {
+        if (s[i] < '0' || s[i] > '9') return 0;
+        major = major * 10 + (s[i] - '0');
+    }
+    auto hex = [](char c) { return c >= '0' && c <= '9' ? c - '0' : c >= 'a' && c <= 'f' ? c - 'a' + 10 : -1; };
+    const int minor = hex(s[n - 2]), stepping = hex(s[n - 1]);
+    if (minor < 0 || stepping < 0) return 0;
+    return major * 100 + minor * 10 + stepping;
+}
+
+extern "C" int32_t w4a16_debug_parse_gcn_arch(const char* name) { return parse_gcn_arch(name); }
+
 extern "C" int w4a16_debug_prefill_occupancy(int cfg, const w4a16_device_limits* lim) {
     if (!lim || cfg < 1 || cfg > kNumPrefillTable) return -1;
     return prefill_occupancy(cfg, *lim);
@@ -364,9 +386,7 @@ extern "C" int w4a16_query_device(int device, w4a16_device_limits* lim) {
     l.cu_count = prop.multiProcessorCount;
     l.lds_bytes_per_block = (int32_t)prop.sharedMemPerBlock;
     l.max_threads_per_block = prop.maxThreadsPerBlock;
-    l.gcn_arch = 0;
-    const char* a = prop.gcnArchName;                      // e.g. "gfx950:sramecc+:xnack-"
-    if (a && std::strncmp(a, "gfx", 3) == 0) l.gcn_arch = (int32_t)std::strtol(a + 3, nullptr, 10);
+    l.gcn_arch = parse_gcn_arch(prop.gcnArchName);         // e.g. "gfx950:sramecc+:xnack-" -> 950
     cache[device] = l;
     *lim = l;
     return W4A16_OK;
