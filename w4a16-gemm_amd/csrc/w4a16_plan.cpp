@@ -257,7 +257,12 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             //    traffic per block grows, two-block tiles of 4 waves split in two (M = 16: 11.95
             //    vs 12.57 us for 8 waves, in two sweeps);
             //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves, else two-block
-            //    rings of 4.
+            //    rings of 4;
+            //  * more single-block tiles than CUs (qkv N = 6144, Llama-3-70B down N = 8192): two-block
+            //    rings of 8 waves from 2 token rows up, which give every CU one tile (70B down
+            //    M = 8: 28.5 vs 33.2 us for the single-block rings; qkv M = 8: 6.08 vs 6.46 us);
+            //    16 waves at M <= 4 on long K (70B down M = 4: 26.3 vs 27.7 us), 4-block rings of 4
+            //    waves split in two above 8 rows (70B down M = 16: 30.6 vs 35.6 us).
             // Above 8 token rows a ring's LDS allows one or two workgroups per CU, so a shape is
             // taken only if all its workgroups are resident at once (qkv, N = 6144, M = 16: 6.7
             // vs 9.4 us for the single-block rings, whose 384 workgroups ran in two rounds).
@@ -280,13 +285,20 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             Cand longk_large_m[] = {{20, 2}, {22, 2}, {19, 1}};
             Cand shortk_m1[] = {{29, 1}, {19, 1}, {14, 1}};
             Cand shortk[] = {{19, 1}, {20, 1}, {21, 1}};
+            Cand many_m1[] = {{26, 1}, {29, 1}, {19, 1}};
+            Cand many_longk_m4[] = {{30, 1}, {26, 1}, {29, 1}};
+            Cand many_small_m[] = {{26, 1}, {22, 1}, {19, 1}};
+            Cand many_longk_large_m[] = {{16, 2}, {26, 1}, {20, 2}};
             Cand* list;
             const int n = 3;
             const bool very_wide = (int64_t)ntiles_of(12) * 2 >= 3LL * cus;
+            const bool many_blocks = N / 16 > cus;                      // single-block tiles: over one per CU
             if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus)
                 list = M <= 1 && very_wide ? vwide_m1 : M <= 4 ? (very_wide ? vwide_small_m : wide_small_m) : wide;
+            else if (KC >= 128 && many_blocks)
+                list = M <= 1 ? many_m1 : M <= 4 ? many_longk_m4 : M <= 8 ? many_small_m : many_longk_large_m;
             else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
-            else list = M <= 1 ? shortk_m1 : shortk;
+            else list = M <= 1 ? shortk_m1 : M <= 8 && many_blocks ? many_small_m : shortk;
             for (int i = 0; i < n && var < 0; ++i)
                 if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus &&
                     (M <= 8 || one_round(list[i].v, list[i].sp))) {
