@@ -170,7 +170,8 @@ def _kernels(text):
 def test_untracked_load_registers_untouched_until_waited(isa):
     ks = _kernels(isa)
     lds = [k for k in ks if any(n in k for n in ("decode_stream_kernel", "decode_ring_kernel",
-                                                  "prefill_wide_kernel", "prefill_stream_kernel",
+                                                  "prefill_wide_kernel", "prefill_wide_pipe_kernel",
+                                                  "prefill_stream_kernel",
                                                   "prefill_group_kernel"))]
     assert len(lds) >= 16 + 20 + 3 + 2 + 2, list(ks)
     problems = {k: check_kernel(ks[k]) for k in lds}
@@ -236,11 +237,11 @@ def test_wide_prefill_accumulators_stay_in_place(isa):
     """The wide prefill main loop keeps its MFMA accumulators in place: no accumulator register
     copies or AGPR<->VGPR transfers (the default scheduler's allocation rotated them through
     copies, serialising the MFMA pipe)."""
-    ks = {k: v for k, v in _kernels(isa).items() if "prefill_wide_kernel" in k}
-    # seven configs, five of them also with the second accumulator set of the long-K segments
-    # (Lb1E; checked for spills and load hazards by the tests above, their loop holds the
-    # segment-close branch)
-    assert len(ks) == 12 and sum("Lb1E" in k for k in ks) == 5, list(ks)
+    ks = {k: v for k, v in _kernels(isa).items() if "prefill_wide_kernel" in k or "prefill_wide_pipe_kernel" in k}
+    # nine configs (two of them the pipelined kernel), five of them also with the second
+    # accumulator set of the long-K segments (Lb1E; checked for spills and load hazards by the
+    # tests above, their loop holds the segment-close branch)
+    assert len(ks) == 14 and sum("Lb1E" in k for k in ks) == 5, list(ks)
     for name, lines in ks.items():
         if "Lb1E" in name:
             continue

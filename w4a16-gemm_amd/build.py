@@ -13,6 +13,7 @@ Outputs (next to this file, git-ignored, shipped to the GPU box with the tree):
 from __future__ import annotations
 
 import argparse
+import concurrent.futures
 import os
 import subprocess
 import sys
@@ -68,11 +69,13 @@ def build_lib() -> str:
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
-    for src, _ in SOURCES:
-        obj = os.path.join(objdir, src.rsplit(".", 1)[0] + ".o")
-        _run([hipcc, *compile_flags(src), "-c", os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+    objs = [os.path.join(objdir, src.rsplit(".", 1)[0] + ".o") for src, _ in SOURCES]
+    # the translation units compile independently: in parallel (the kernels file is the long pole)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+        jobs = [pool.submit(_run, [hipcc, *compile_flags(src), "-c", os.path.join(CSRC, src), "-o", obj])
+                for (src, _), obj in zip(SOURCES, objs)]
+        for job in jobs:
+            job.result()
     tmp = LIB + ".tmp"
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)

@@ -20,9 +20,9 @@ namespace w4a16 {
 //        slots), the value hipOccupancyMaxActiveBlocksPerMultiprocessor reports for it
 //        (tests/test_w4a16_gpu.py::test_planner_occupancy_matches_the_compiled_kernels).
 struct PrefillTile {
-    int bm, bn, waves_m, waves_n, kind, depth, wpe, occ;
+    int bm, bn, waves_m, waves_n, kind, depth, wpe, occ, pipe;
 };
-constexpr PrefillTile kPrefillTable[22] = {
+constexpr PrefillTile kPrefillTable[24] = {
     {0, 0, 0, 0, 0, 0, 0, 0},
     {16, 128, 1, 4, 0, 0, 0, 7},     // 1: small batches: 4 waves across N, wave tile 16 x 32
     {32, 128, 1, 4, 0, 0, 0, 6},     // 2: wave tile 32 x 32
@@ -45,9 +45,11 @@ constexpr PrefillTile kPrefillTable[22] = {
     {64, 256, 1, 8, 1, 2, 2, 2},     // 19: wave tile 64 x 32, 8 waves across N share the x rows
     {128, 128, 1, 4, 1, 4, 2, 2},    // 20: wave tile 128 x 32, 4 waves across N
     {256, 256, 2, 4, 1, 2, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves
+    {64, 128, 1, 4, 1, 4, 2, 2, 1},  // 22: config 18 software-pipelined across chunks (three x buffers)
+    {64, 256, 1, 8, 1, 2, 2, 1, 1},  // 23: config 19 software-pipelined across chunks
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 21;     // all prefill configs
+constexpr int kNumPrefillTable = 23;     // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;
@@ -66,7 +68,7 @@ constexpr int prefill_lds_bytes(int cfg) {
            : kPrefillTable[cfg].kind == 2
                ? (kPrefillTable[cfg].depth + 1) *
                      (2048 * kPrefillTable[cfg].waves_n + kPrefillTable[cfg].bm / 4 * 1024)   // ring slots
-               : 2 * kPrefillTable[cfg].bm * kLdsRowBytes;
+               : (kPrefillTable[cfg].pipe ? 3 : 2) * kPrefillTable[cfg].bm * kLdsRowBytes;
 }
 // Canonical prefill accumulation order.  Every prefill config sums the K range in the same
 // order, so all of them give bit-identical results and token rows are independent of M:
@@ -89,7 +91,7 @@ constexpr int prefill_segments(int KC) {
 // Whether a kind-1 config has the registers for a second accumulator set: not the 128 x 64
 // wave tiles budgeted for two waves per SIMD (configs 5 and 21: 128 accumulators in 256 registers).
 constexpr bool prefill_wide_segmentable(int cfg) {
-    return kPrefillTable[cfg].kind == 1 &&
+    return kPrefillTable[cfg].kind == 1 && !kPrefillTable[cfg].pipe &&
            !(kPrefillTable[cfg].wpe == 2 &&
              (kPrefillTable[cfg].bm / kPrefillTable[cfg].waves_m) * (kPrefillTable[cfg].bn / kPrefillTable[cfg].waves_n) >=
                  128 * 64);

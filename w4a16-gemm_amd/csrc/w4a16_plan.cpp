@@ -81,8 +81,9 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //    for 128 x 256; then 128 x 256 (two workgroups per CU); then 128 x 128 with four waves
     //    of 128 x 32 (M >= 128), e.g. N = 28672, M = 128: 43.4 vs 55.4 us for two waves of
     //    128 x 64, N = 4096, K = 14336, M = 1024: 137 vs 171; then 64 x 128 with four waves of
-    //    64 x 32 (M >= 64), e.g. configs[2] (M = 128, N = 14336, G = 64): 29.9 vs 36.4 us for
-    //    token groups of 32, N = 4096, M = 512: 29.4 vs 34.1;
+    //    64 x 32 (M >= 64), software-pipelined across chunks (config 22; the unpipelined config
+    //    18 on long K), e.g. configs[2] (M = 128, N = 14336, G = 64): 27.6 us against 30.7 for
+    //    config 18 and 36.4 for token groups of 32, N = 4096, M = 512: 27.6 vs 29.2 (config 18);
     //  * token groups of 16 rows, one n16 block per wave, 4 pairs in flight, while their waves
     //    (M/16 groups x N/16 blocks) are at most 12 per CU: every small-M shape measured, e.g.
     //    K = 14336, N = 4096, M = 32: 42.8 vs 52.6 us for one wave per block over 32 rows
@@ -124,7 +125,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     }
     if (wide_tiles(5) >= 0.75 * cus) return 5;
     if (M >= 128 && wide_tiles(20) >= 0.75 * cus) return 20;
-    if (M >= 64 && wide_tiles(18) >= 0.75 * cus) return 18;
+    if (M >= 64 && wide_tiles(22) >= 0.75 * cus) return 22;
     const double blocks = std::ceil(N / 16.0);
     if (prefill_occupancy(17, lim) > 0 && prefill_shape_ok(17, M, K) &&
         std::ceil(M / 16.0) * blocks <= 12.0 * cus)

@@ -1,4 +1,4 @@
-// Wide-tile prefill (configs 5..7 and 18..21 of kPrefillTable, kind 1) in its own translation unit.
+// Wide-tile prefill (configs 5..7 and 18..23 of kPrefillTable, kind 1) in its own translation unit.
 //
 // Built with -mllvm -amdgpu-sched-strategy=max-memory-clause (build.py): with the default
 // scheduler the register allocator gives most MFMAs a destination other than their accumulator
@@ -305,7 +305,275 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     }
 }
 
+// The same tiles software-pipelined across chunks, for the 32-channel wave tiles that run one wave
+// per SIMD (few tiles: moderate M).  prefill_wide_kernel serialises each chunk -- x store, B reads
+// after the barrier, dequantisation, then the MFMAs -- and with no second wave on the SIMD every
+// latency in that chain is exposed (configs[2]: ~1000 cycles per chunk for 256 cycles of MFMA).
+// Here x has three LDS buffers, so the barrier that ends chunk c-1 has already published x of
+// chunk c+1, and during chunk c's MFMAs each wave
+//  * reads chunk c+1's B operands from LDS into a second register set,
+//  * dequantises chunk c+1's weights (loaded R chunks ahead) into a second set of A operands,
+//  * stores x of chunk c+2 into the third buffer and issues the loads R chunks ahead.
+// Chunk c uses x buffer c % 3 (a wave-uniform rotation) and register sets c % R (static: the loop
+// is unrolled by R).  In flight when chunk c starts, oldest first: x c+2, weights c+1, x c+3,
+// weights c+2, ..., x c+1+R, weights c+R.  Each accumulator receives exactly the MFMA sequence of
+// prefill_wide_kernel (chunk by chunk, h = 0 then 1, tp = 0 then 1, same A and B operands), so
+// the output is bit-identical to every other prefill config.  One K chain only (K <= 8192): the
+// second register sets leave no room for the long-K segments' second accumulator set.
+// Measured on MI355X against the same tiles unpipelined: 6-10% faster at M = 64..512 (configs[2]:
+// 30.7 -> 27.6 us); loads eight chunks ahead, or MFMAs and dequantisation interleaved one by one
+// (sched_group_barrier), were no faster.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE, bool SEG, int R>
+__global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+prefill_wide_pipe_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
+                         const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
+                         int M, int N, int K, int gshift, int tiles_m, int group_m, int seg_chunks) {
+    constexpr int NT = WAVES_M * WAVES_N * 64;
+    constexpr int WM = BM / WAVES_M;
+    constexpr int WN = BN / WAVES_N;
+    constexpr int TM = WM / 32;
+    constexpr int TN = WN / 32;
+    constexpr int XBUF = BM * kXRow;
+    constexpr int SEGS = BM * 8;
+    constexpr int SPT = SEGS / NT;
+    static_assert(WM % 32 == 0 && WN % 32 == 0 && SEGS % NT == 0, "tile shape");
+    static_assert(R == 2 || R == 4, "register sets: the A/B operand sets alternate with the chunk parity");
+    static_assert(!SEG, "one K chain only: the pipelined tiles are not used above K = 8192 (no registers for a second set)");
+    __shared__ __attribute__((aligned(16))) char xs[3 * XBUF];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N;
+    const int wn = wave - wm * WAVES_N;
+    const int kg = lane >> 5;
+    const int r = lane & 31;
+
+    // Tile order as in prefill_wide_kernel (XCD-contiguous, groups of group_m M tiles).
+    const int G = gridDim.x;
+    const int G8 = G >> 3;
+    const int b = blockIdx.x;
+    const int tile = b < (G8 << 3) ? (b & 7) * G8 + (b >> 3) : b;
+    const int tiles_n = G / tiles_m;
+    const int gid = tile / (group_m * tiles_n);
+    const int first_m = gid * group_m;
+    const int gsz = min(tiles_m - first_m, group_m);
+    const int rem = tile - gid * group_m * tiles_n;
+    const int tm = first_m + rem % gsz;
+    const int tn = rem / gsz;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    const int KC = K >> 6;
+    const int NBLK = N >> 4;
+    const int nb0 = (n0 + wn * WN) >> 4;
+
+    // Load addressing as in prefill_wide_kernel: wave-uniform bases, constant per-lane offsets,
+    // rows past M and blocks past N clamped in bounds.
+    const char* wbase[TN];
+    const char* sbase[TN];
+    int qblk[TN];
+#pragma unroll
+    for (int q = 0; q < TN; ++q) {
+        qblk[q] = min(nb0 + 2 * q, NBLK - 1);
+        wbase[q] = reinterpret_cast<const char*>(Wp + (size_t)qblk[q] * KC * 32);
+        sbase[q] = reinterpret_cast<const char*>(scales + (size_t)qblk[q] * 16);
+    }
+    uint32_t woff[TN][2];
+    uint32_t soff[TN];
+#pragma unroll
+    for (int q = 0; q < TN; ++q) {
+        const int nbl = min(nb0 + 2 * q + (r >> 4), NBLK - 1) - qblk[q];
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+            woff[q][tp] = (uint32_t)(nbl * KC * 512 + (((r & 7) << 2) | (tp << 1) | kg) * 16);
+        soff[q] = (uint32_t)((nbl * 16 + (r & 15)) * 2);
+    }
+    const char* xbase = reinterpret_cast<const char*>(x + (size_t)m0 * K);
+    uint32_t xoff[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+        const int sg = tid + i * NT;
+        xoff[i] = ((uint32_t)(min(m0 + (sg >> 3), M - 1) - m0) * (uint32_t)K + (sg & 7) * 8) * 2;
+    }
+
+    u4 xr[R][SPT];
+    auto load_x = [&](int kc, u4 (&xv)[SPT]) __attribute__((always_inline)) {
+        const char* xb = xbase + (size_t)min(kc, KC - 1) * 128;
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) xv[i] = gload_u4_sbase(xb, xoff[i]);
+    };
+    auto store_x = [&](int buf, u4 (&xv)[SPT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) bind_after_wait(xv[i]);
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int sg = tid + i * NT;
+            lds_store_xseg(xs + buf * XBUF + (sg >> 3) * kXRow, sg & 7, xv[i]);
+        }
+    };
+    u4 wr[R][TN][2];
+    uint32_t sr[R][TN];
+    auto load_w = [&](int kc, u4 (&w)[TN][2], uint32_t (&s)[TN]) __attribute__((always_inline)) {
+        const int kcl = min(kc, KC - 1);
+#pragma unroll
+        for (int q = 0; q < TN; ++q)
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp) w[q][tp] = gload_u4_sbase(wbase[q] + (size_t)kcl * 512, woff[q][tp]);
+#pragma unroll
+        for (int q = 0; q < TN; ++q) s[q] = gload_u16_sbase(sbase[q] + (size_t)(kcl >> gshift) * N * 2, soff[q]);
+    };
+    constexpr int WAIT_X = 3 * TN + (R - 1) * (SPT + 3 * TN);
+    constexpr int WAIT_W = (R - 1) * (SPT + 3 * TN) + SPT;
+    static_assert(WAIT_X <= 63 && WAIT_W <= 63, "vmcnt range");
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int p = 0; p < TM; ++p)
+#pragma unroll
+        for (int q = 0; q < TN; ++q)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[p][q][i] = 0.f;
+
+    const Dq d = dq_setup(r);
+    const uint32_t xrow = (uint32_t)reinterpret_cast<uintptr_t>(xs) + (wm * WM + r) * kXRow + kg * 16;
+    u4 bv[2][TM][2][2];                                        // B operands [set][p][h][tp]
+    h8 av[2][TN][2][2];                                        // A operands [set][q][h][tp]
+    auto read_b = [&](int buf, u4 (&bo)[TM][2][2]) __attribute__((always_inline)) {
+        const uint32_t xb = xrow + buf * XBUF;
+#pragma unroll
+        for (int p = 0; p < TM; ++p)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp) bo[p][h][tp] = lds_read_u4(xb + p * 32 * kXRow + h * 64 + tp * 32);
+    };
+    auto bind_b = [&](u4 (&bo)[TM][2][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < TM; ++p)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) { bind_after_wait(bo[p][h][0]); bind_after_wait(bo[p][h][1]); }
+    };
+    auto bind_w = [&](u4 (&w)[TN][2], uint32_t (&s)[TN]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+            bind_after_wait(w[q][0]); bind_after_wait(w[q][1]); bind_after_wait(s[q]);
+        }
+    };
+    auto dequant = [&](u4 (&w)[TN][2], uint32_t (&s)[TN], h8 (&a)[TN][2][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+            const h2 s2 = scale2((uint16_t)s[q]);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp) {
+                a[q][0][tp] = dq_frag(w[q][tp].x, w[q][tp].y, d, s2);
+                a[q][1][tp] = dq_frag(w[q][tp].z, w[q][tp].w, d, s2);
+            }
+        }
+    };
+    auto mma = [&](u4 (&bo)[TM][2][2], h8 (&a)[TN][2][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int p = 0; p < TM; ++p) {
+                    const h8 bf = __builtin_bit_cast(h8, bo[p][h][tp]);
+#pragma unroll
+                    for (int q = 0; q < TN; ++q) acc[p][q] = mfma32x32x16(a[q][h][tp], bf, acc[p][q]);
+                }
+    };
+
+    // Prologue: x of chunks 0 and 1 into buffers 0 and 1, chunk 0's operands into set 0, then
+    // the loads x 2, w 1, ..., x R+1, w R (register sets 2 % R.. and 1.. once their data is used).
+    load_x(0, xr[0]);
+    load_x(1, xr[1]);
+    load_w(0, wr[0], sr[0]);
+    wait_vmcnt<0>();
+    store_x(0, xr[0]);
+    store_x(1, xr[1]);
+    __syncthreads();
+    read_b(0, bv[0]);
+    bind_w(wr[0], sr[0]);
+    dequant(wr[0], sr[0], av[0]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    bind_b(bv[0]);
+    static_for<2, R + 2>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        load_x(J, xr[J % R]);
+        load_w(J - 1, wr[(J - 1) % R], sr[(J - 1) % R]);
+    });
+    int b1 = 1, b2 = 2;                                        // x buffers of chunks c+1, c+2
+    for (int kc = 0; kc < KC; kc += R) {
+        static_for<0, R>([&](auto t) {
+            constexpr int T = decltype(t)::value;
+            constexpr int CUR = T & 1;
+            const int c = kc + T;
+            read_b(b1, bv[CUR ^ 1]);                           // B of chunk c+1
+            wait_vmcnt<WAIT_X>();                              // x of chunk c+2 has landed
+            store_x(b2, xr[(T + 2) % R]);
+            load_x(c + 2 + R, xr[(T + 2) % R]);
+            wait_vmcnt<WAIT_W>();                              // weights of chunk c+1 have landed
+            bind_w(wr[(T + 1) % R], sr[(T + 1) % R]);
+            mma(bv[CUR], av[CUR]);                             // chunk c
+            dequant(wr[(T + 1) % R], sr[(T + 1) % R], av[CUR ^ 1]);
+            load_w(c + 1 + R, wr[(T + 1) % R], sr[(T + 1) % R]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            bind_b(bv[CUR ^ 1]);
+            __builtin_amdgcn_s_barrier();                      // publishes x c+2, retires reads of x c+1's predecessor
+            b1 = b2;
+            b2 = b2 == 2 ? 0 : b2 + 1;
+        });
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) bind_after_wait(xr[j][i]);
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+            bind_after_wait(wr[j][q][0]); bind_after_wait(wr[j][q][1]); bind_after_wait(sr[j][q]);
+        }
+
+    int lane_e;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+    const int r_e = lane_e & 31;
+    const int kg_e = lane_e >> 5;
+#pragma unroll
+    for (int p = 0; p < TM; ++p) {
+        const int m = m0 + wm * WM + p * 32 + r_e;
+        if (m >= M) continue;
+#pragma unroll
+        for (int q = 0; q < TN; ++q) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int nbk = nb0 + 2 * q + (g >> 1);
+                const int n = (nb0 + 2 * q) * 16 + 8 * g + 4 * kg_e;
+                if (nbk < NBLK)
+                    *reinterpret_cast<u2*>(y + (size_t)m * N + n) =
+                        pack_f16x4(f4{acc[p][q][4 * g], acc[p][q][4 * g + 1], acc[p][q][4 * g + 2], acc[p][q][4 * g + 3]});
+            }
+        }
+    }
+}
+
 constexpr int kWideGroupM = 4;                                 // M tiles per group of the tile order
+
+template <int CFG, bool SEG>
+static void launch_wide_kernel(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s, uint16_t* y,
+                               hipStream_t st, int gshift, int tiles_m, int group_m, int seg_chunks) {
+    constexpr PrefillTile c = kPrefillTable[CFG];
+    constexpr int R = prefill_wide_steps(CFG, SEG);
+    if constexpr (c.pipe)
+        hipLaunchKernelGGL((prefill_wide_pipe_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, SEG, R>), dim3(p.grid),
+                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
+                           group_m, seg_chunks);
+    else
+        hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, SEG, R>), dim3(p.grid),
+                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
+                           group_m, seg_chunks);
+}
 
 template <int CFG>
 static hipError_t launch_wide(const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s, uint16_t* y,
@@ -323,15 +591,11 @@ static hipError_t launch_wide(const w4a16_plan& p, const u4* Wp, const uint16_t*
     const int seg_chunks = prefill_segment_chunks(KC);
     if (prefill_segments(KC) > 1) {
         if constexpr (prefill_wide_segmentable(CFG))
-            hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, true, prefill_wide_steps(CFG, true)>), dim3(p.grid),
-                               dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
-                               group_m, seg_chunks);
+            launch_wide_kernel<CFG, true>(p, Wp, x, s, y, st, gshift, tiles_m, group_m, seg_chunks);
         else
             return hipErrorInvalidValue;                      // no registers for a second set (planner never asks)
     } else {
-        hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false, prefill_wide_steps(CFG, false)>), dim3(p.grid),
-                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
-                           group_m, seg_chunks);
+        launch_wide_kernel<CFG, false>(p, Wp, x, s, y, st, gshift, tiles_m, group_m, seg_chunks);
     }
     return hipGetLastError();
 }
@@ -346,6 +610,8 @@ hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const
         case 19: return launch_wide<19>(p, Wp, x, s, y, st);
         case 20: return launch_wide<20>(p, Wp, x, s, y, st);
         case 21: return launch_wide<21>(p, Wp, x, s, y, st);
+        case 22: return launch_wide<22>(p, Wp, x, s, y, st);
+        case 23: return launch_wide<23>(p, Wp, x, s, y, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -355,11 +621,16 @@ hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const
 template <int CFG>
 static int occupancy_wide() {
     constexpr PrefillTile c = kPrefillTable[CFG];
+    constexpr int R = prefill_wide_steps(CFG, false);
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false, prefill_wide_steps(CFG, false)>,
-                                                     c.waves_m * c.waves_n * 64, 0) != hipSuccess)
-        return -1;
-    return n;
+    hipError_t e;
+    if constexpr (c.pipe)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, prefill_wide_pipe_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false, R>, c.waves_m * c.waves_n * 64, 0);
+    else
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, false, R>, c.waves_m * c.waves_n * 64, 0);
+    return e == hipSuccess ? n : -1;
 }
 
 int prefill_wide_occupancy(int cfg) {
@@ -371,6 +642,8 @@ int prefill_wide_occupancy(int cfg) {
         case 19: return occupancy_wide<19>();
         case 20: return occupancy_wide<20>();
         case 21: return occupancy_wide<21>();
+        case 22: return occupancy_wide<22>();
+        case 23: return occupancy_wide<23>();
         default: return -1;
     }
 }

@@ -208,7 +208,8 @@ py::dict w4a16_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int64_t var
             const bool segs = w4a16::prefill_segments((int)(K / 64)) > 1;
             const char* seg = segs ? "true" : "false";
             if (t.kind == 1) {
-                std::string n = tmpl("prefill_wide_kernel", {t.bm, t.bn, t.waves_m, t.waves_n, t.wpe}, seg);
+                std::string n = tmpl(t.pipe ? "prefill_wide_pipe_kernel" : "prefill_wide_kernel",
+                                     {t.bm, t.bn, t.waves_m, t.waves_n, t.wpe}, seg);
                 d["kernel_name"] = n.substr(0, n.size() - 1) + ", " +
                                    std::to_string(w4a16::prefill_wide_steps(plan.kernel, segs)) + ">";
             }
