@@ -1,4 +1,4 @@
-// Wide-tile prefill (configs 5..7 and 18..23 of kPrefillTable, kind 1) in its own translation unit.
+// Wide-tile prefill (configs 5..7 and 18..22 of kPrefillTable, kind 1) in its own translation unit.
 //
 // Built with -mllvm -amdgpu-sched-strategy=max-memory-clause (build.py): with the default
 // scheduler the register allocator gives most MFMAs a destination other than their accumulator
@@ -611,7 +611,6 @@ hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const
         case 20: return launch_wide<20>(p, Wp, x, s, y, st);
         case 21: return launch_wide<21>(p, Wp, x, s, y, st);
         case 22: return launch_wide<22>(p, Wp, x, s, y, st);
-        case 23: return launch_wide<23>(p, Wp, x, s, y, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -643,7 +642,6 @@ int prefill_wide_occupancy(int cfg) {
         case 20: return occupancy_wide<20>();
         case 21: return occupancy_wide<21>();
         case 22: return occupancy_wide<22>();
-        case 23: return occupancy_wide<23>();
         default: return -1;
     }
 }
