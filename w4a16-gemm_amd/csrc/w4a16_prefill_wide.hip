@@ -186,19 +186,22 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // One chunk: for each half h, the 2 TM B operands are read from LDS through asm (the compiler
     // would follow each read with a full lgkmcnt wait), the 2 TN A operands are dequantised
     // while the reads are in flight, then one wait and the 4 TM TN MFMAs (tp = 0 before tp = 1).
-    auto compute = [&](int buf, u4 (&w)[TN][2], uint32_t (&s)[TN]) __attribute__((always_inline)) {
+    // The buffer and every B-operand offset are compile-time constants carried in the ds_read
+    // offset field (no address arithmetic per read).
+    auto compute = [&](auto buf, u4 (&w)[TN][2], uint32_t (&s)[TN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < TN; ++q) {
             bind_after_wait(w[q][0]); bind_after_wait(w[q][1]); bind_after_wait(s[q]);
         }
-        const uint32_t xb = xrow + buf * XBUF;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        static_for<0, 2>([&](auto hh) {
+            constexpr int h = decltype(hh)::value;
             u4 bv[TM][2];
-#pragma unroll
-            for (int p = 0; p < TM; ++p)
-#pragma unroll
-                for (int tp = 0; tp < 2; ++tp) bv[p][tp] = lds_read_u4(xb + p * 32 * kXRow + h * 64 + tp * 32);
+            static_for<0, TM>([&](auto pp) {
+                constexpr int P = decltype(pp)::value;
+                constexpr int O = decltype(buf)::value * XBUF + P * 32 * kXRow + h * 64;
+                bv[P][0] = lds_read_u4_at<O>(xrow);
+                bv[P][1] = lds_read_u4_at<O + 32>(xrow);
+            });
             h8 a[TN][2];
 #pragma unroll
             for (int q = 0; q < TN; ++q) {
@@ -218,7 +221,7 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
                     for (int q = 0; q < TN; ++q) acc[p][q] = mfma32x32x16(a[q][tp], bf, acc[p][q]);
                 }
-        }
+        });
     };
 
     // Issue order: prologue x0 | x1 w0 x2 w1 ... x(R) w(R-1); then chunk c issues x(c+1+R) and
@@ -245,7 +248,7 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             store_x((T + 1) & 1, xr[(T + 1) % R]);
             load_x(c + 1 + R, xr[(T + 1) % R]);
             wait_vmcnt<WAIT_W>();
-            compute(T & 1, wr[T], sr[T]);
+            compute(std::integral_constant<int, T & 1>{}, wr[T], sr[T]);
             load_w(c + R, wr[T], sr[T]);
             __syncthreads();
         });
@@ -439,13 +442,14 @@ prefill_wide_pipe_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__
     u4 bv[2][TM][2][2];                                        // B operands [set][p][h][tp]
     h8 av[2][TN][2][2];                                        // A operands [set][q][h][tp]
     auto read_b = [&](int buf, u4 (&bo)[TM][2][2]) __attribute__((always_inline)) {
-        const uint32_t xb = xrow + buf * XBUF;
-#pragma unroll
-        for (int p = 0; p < TM; ++p)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int tp = 0; tp < 2; ++tp) bo[p][h][tp] = lds_read_u4(xb + p * 32 * kXRow + h * 64 + tp * 32);
+        const uint32_t xb = xrow + buf * XBUF;                 // the offsets within the buffer are immediates
+        static_for<0, TM>([&](auto pp) {
+            constexpr int P = decltype(pp)::value;
+            bo[P][0][0] = lds_read_u4_at<P * 32 * kXRow>(xb);
+            bo[P][0][1] = lds_read_u4_at<P * 32 * kXRow + 32>(xb);
+            bo[P][1][0] = lds_read_u4_at<P * 32 * kXRow + 64>(xb);
+            bo[P][1][1] = lds_read_u4_at<P * 32 * kXRow + 96>(xb);
+        });
     };
     auto bind_b = [&](u4 (&bo)[TM][2][2]) __attribute__((always_inline)) {
 #pragma unroll
