@@ -181,7 +181,8 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (32, 28672, 4096, 10),                                                   # token groups of 32
     # long K (4 or 7 segments): split-K token groups, larger groups sooner
     (64, 4096, 14336, 10), (128, 4096, 14336, 12), (256, 4096, 14336, 13), (512, 4096, 14336, 18),
-    (17, 8192, 28672, 12), (192, 8192, 28672, 13), (384, 8192, 28672, 19), (2048, 8192, 28672, 20),
+    (17, 8192, 28672, 12), (192, 8192, 28672, 13), (384, 8192, 28672, 19), (2048, 8192, 28672, 7),
+    (2048, 4096, 14336, 7), (1024, 8192, 28672, 7),                         # long K, >= 2 rounds of 128 x 128: two 128 x 64 waves
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)

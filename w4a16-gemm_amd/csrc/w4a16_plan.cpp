@@ -102,6 +102,10 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     // the fastest forced config: e.g. K = 14336, N = 4096, M = 32: 19.2 us (42.8 us before the
     // segments), M = 64: 25.9 (groups of 32, one block per wave), M = 128: 38.8 (groups of 32,
     // two blocks per wave), M = 256: 58.1 (groups of 64), M = 512: 94.6 (64 x 128 wide tiles).
+    // At M >= 1024, two waves of 128 x 64 per 128 x 128 tile (config 7, one wave per SIMD) once
+    // its tiles fill two rounds of the CUs' workgroup slots (K = 14336, N = 4096, M = 2048: 237 vs
+    // 252 us for four waves of 128 x 32; K = 28672, N = 8192, M = 1024: 472 vs 499), else the four
+    // 128 x 32 waves (K = 14336, N = 4096, M = 1024: 143 vs 180 us).
     const int segs = prefill_segments(K / 64);
     if (segs > 1) {
         auto group_waves = [&](int cfg) {
@@ -109,6 +113,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
             return std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn) * t.waves_n * segs;
         };
         auto group_ok = [&](int cfg) { return prefill_occupancy(cfg, lim) > 0 && prefill_shape_ok(cfg, M, K); };
+        if (M >= 1024 && wide_tiles(7) >= 2.0 * cus) return 7;
         if (M >= 1024 && wide_tiles(20) >= 0.75 * cus) return 20;
         if (M >= 384 && wide_tiles(19) >= 0.75 * cus) return 19;
         if (M >= 256 && wide_tiles(18) >= 0.75 * cus) return 18;
