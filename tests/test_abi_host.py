@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 22
+        assert 1 <= p.kernel <= 23
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -165,13 +165,15 @@ def test_prefill_plan_invariants(lib, M, N):
 PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128),
                  8: (32, 16), 9: (64, 16), 10: (32, 64), 11: (64, 64), 12: (32, 128), 13: (64, 128), 14: (32, 128),
                  15: (32, 256), 16: (16, 64), 17: (16, 64), 18: (64, 128), 19: (64, 256), 20: (128, 128),
-                 21: (256, 256), 22: (64, 128)}
+                 21: (256, 256), 22: (64, 128), 23: (128, 512)}
 
 
 @pytest.mark.parametrize("M,N,K,want", [
-    (2048, 28672, 8192, 5), (4096, 4096, 4096, 5),                           # 128x256 tiles fill whole rounds
+    (2048, 28672, 8192, 5), (1280, 28672, 4096, 5), (4096, 6144, 4096, 5),   # 128x512 last round half full or less
     (1024, 6144, 4096, 5),                                                   # >= 3/4 of the CUs: 128x256
-    (2048, 14336, 4096, 21), (512, 28672, 8192, 21), (2048, 6144, 4096, 21), # <= 2 rounds of 256x256 tiles
+    (2048, 14336, 4096, 23), (512, 28672, 8192, 23), (2048, 6144, 4096, 23), # 128x512: last round > half full
+    (1024, 28672, 8192, 23), (4096, 4096, 4096, 23), (1536, 28672, 4096, 23), (768, 14336, 4096, 23),
+    (768, 28672, 4096, 5),
     (1024, 4096, 4096, 20), (1024, 4096, 14336, 20),                         # 128 tiles of 128x256: 128x128
     (512, 6144, 4096, 20), (256, 14336, 4096, 20), (128, 28672, 4096, 20),   # 128x128, four 128x32 waves
     (128, 14336, 4096, 22), (512, 4096, 4096, 22), (64, 28672, 4096, 22),    # 64x128, four 64x32 waves, pipelined
@@ -194,7 +196,7 @@ def test_prefill_wide_selection(lib, M, N, K, want):
     tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1]) * max(p.splits, 1)
     assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4, 12: 4, 13: 4, 14: 4,
-                            15: 4, 16: 4, 17: 4, 18: 4, 19: 8, 20: 4, 21: 8, 22: 4}[p.kernel]
+                            15: 4, 16: 4, 17: 4, 18: 4, 19: 8, 20: 4, 21: 8, 22: 4, 23: 8}[p.kernel]
 
 
 def test_prefill_override(lib, monkeypatch):
@@ -301,12 +303,12 @@ def test_bandwidth_probe_loads_and_rejects_bad_arguments():
 
 def test_planner_occupancy_hook_covers_every_prefill_config(lib):
     lib.w4a16_debug_prefill_occupancy.argtypes = [ctypes.c_int, ctypes.POINTER(Limits)]
-    occ = [lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(MI355X)) for cfg in range(1, 23)]
+    occ = [lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(MI355X)) for cfg in range(1, 24)]
     assert all(o >= 1 for o in occ), occ
     assert lib.w4a16_debug_prefill_occupancy(0, ctypes.byref(MI355X)) == -1
-    assert lib.w4a16_debug_prefill_occupancy(23, ctypes.byref(MI355X)) == -1
+    assert lib.w4a16_debug_prefill_occupancy(24, ctypes.byref(MI355X)) == -1
     older = Limits(256, 64 * 1024, 1024, 942)                # 64 KB of LDS per CU bounds every config
-    assert all(lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(older)) <= o for cfg, o in zip(range(1, 23), occ))
+    assert all(lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(older)) <= o for cfg, o in zip(range(1, 24), occ))
 
 
 @pytest.mark.parametrize("name,want", [
@@ -360,7 +362,7 @@ def test_long_k_plans_split_token_group_configs_by_segment(lib, monkeypatch, M, 
             assert (p.splits, p.grid, p.counter_slots, p.workspace_bytes) == (segs, tiles * segs, tiles, segs * M * N * 4)
         else:
             assert (p.splits, p.grid, p.counter_slots, p.workspace_bytes) == (1, tiles, 0, 0)
-    for cfg in (5, 21, 22):                        # no registers for the second set
+    for cfg in (5, 21, 22, 23):                    # no registers for the second set
         monkeypatch.setenv("W4A16_PREFILL", str(cfg))
         rc, p, err = plan(lib, M=2048, N=4096, K=14336, G=128)
         assert rc == 0 and p.kernel != cfg

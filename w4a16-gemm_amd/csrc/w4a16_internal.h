@@ -22,7 +22,7 @@ namespace w4a16 {
 struct PrefillTile {
     int bm, bn, waves_m, waves_n, kind, depth, wpe, occ, pipe;
 };
-constexpr PrefillTile kPrefillTable[23] = {
+constexpr PrefillTile kPrefillTable[24] = {
     {0, 0, 0, 0, 0, 0, 0, 0},
     {16, 128, 1, 4, 0, 0, 0, 7},     // 1: small batches: 4 waves across N, wave tile 16 x 32
     {32, 128, 1, 4, 0, 0, 0, 6},     // 2: wave tile 32 x 32
@@ -44,11 +44,12 @@ constexpr PrefillTile kPrefillTable[23] = {
     {64, 128, 1, 4, 1, 4, 2, 2},     // 18: wave tile 64 x 32, 4 waves across N
     {64, 256, 1, 8, 1, 2, 2, 2},     // 19: wave tile 64 x 32, 8 waves across N share the x rows
     {128, 128, 1, 4, 1, 4, 2, 2},    // 20: wave tile 128 x 32, 4 waves across N
-    {256, 256, 2, 4, 1, 2, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves
+    {256, 256, 2, 4, 1, 2, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves (forced only)
     {64, 128, 1, 4, 1, 4, 2, 2, 1},  // 22: config 18 software-pipelined across chunks (three x buffers)
+    {128, 512, 1, 8, 1, 2, 2, 1},    // 23: wave tile 128 x 64, 8 waves across N share the x rows
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 22;     // all prefill configs
+constexpr int kNumPrefillTable = 23;     // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;
@@ -88,7 +89,7 @@ constexpr int prefill_segments(int KC) {
     return KC <= 0 ? 1 : (KC + prefill_segment_chunks(KC) - 1) / prefill_segment_chunks(KC);
 }
 // Whether a kind-1 config has the registers for a second accumulator set: not the 128 x 64
-// wave tiles budgeted for two waves per SIMD (configs 5 and 21: 128 accumulators in 256 registers).
+// wave tiles budgeted for two waves per SIMD (configs 5, 21 and 23: 128 accumulators in 256 registers).
 constexpr bool prefill_wide_segmentable(int cfg) {
     return kPrefillTable[cfg].kind == 1 && !kPrefillTable[cfg].pipe &&
            !(kPrefillTable[cfg].wpe == 2 &&

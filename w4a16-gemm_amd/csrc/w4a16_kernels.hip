@@ -1202,6 +1202,7 @@ W4A16_PREFILL_CFG(19)
 W4A16_PREFILL_CFG(20)
 W4A16_PREFILL_CFG(21)
 W4A16_PREFILL_CFG(22)
+W4A16_PREFILL_CFG(23)
 #undef W4A16_PREFILL_CFG
 
 template <int CFG>
@@ -1436,6 +1437,7 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
             case 20: e = launch_prefill<20>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
             case 21: e = launch_prefill<21>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
             case 22: e = launch_prefill<22>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 23: e = launch_prefill<23>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }
@@ -1472,6 +1474,7 @@ extern "C" int w4a16_debug_kernel_occupancy(int cfg) {
         case 20: return prefill_occupancy_of<20>();
         case 21: return prefill_occupancy_of<21>();
         case 22: return prefill_occupancy_of<22>();
+        case 23: return prefill_occupancy_of<23>();
         default: return -1;
     }
 }

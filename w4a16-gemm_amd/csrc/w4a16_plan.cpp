@@ -75,15 +75,24 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     };
     // Rules measured on MI355X (w4a16-gemm_amd/route_sweep.py: every config forced, graph-timed,
     // on the Llama-3-8B projections and the BASELINE shapes, M = 17..2048):
-    //  * the wide 32x32x16 tiles first, largest first, once their tiles number at least 3/4 of
-    //    the CUs and the M tile is filled: 256 x 256 (8 waves, wave tile 128 x 64) while at most
-    //    two rounds of them (M = 256..2048), e.g. N = 28672, K = 8192, M = 512: 230 vs 241 us
-    //    for 128 x 256; then 128 x 256 (two workgroups per CU); then 128 x 128 with four waves
-    //    of 128 x 32 (M >= 128), e.g. N = 28672, M = 128: 43.4 vs 55.4 us for two waves of
-    //    128 x 64, N = 4096, K = 14336, M = 1024: 137 vs 171; then 64 x 128 with four waves of
-    //    64 x 32 (M >= 64), software-pipelined across chunks (config 22; the unpipelined config
-    //    18 on long K), e.g. configs[2] (M = 128, N = 14336, G = 64): 27.6 us against 30.7 for
-    //    config 18 and 36.4 for token groups of 32, N = 4096, M = 512: 27.6 vs 29.2 (config 18);
+    //  * the wide 32x32x16 tiles first, largest first, once the M tile is filled:
+    //    - 128 x 512 (eight 128 x 64 waves sharing the x rows, one workgroup per CU) when the last
+    //      round of its tiles is more than half full (tiles / CUs in (k + 1/2, k + 1]): a full
+    //      round of it runs ~5-9% faster than the same work as 128 x 256 tiles two per CU, but a
+    //      128 x 256 tile alone on a CU finishes a sparse last round in about half a round.
+    //      Measured at M = 256..4096, N = 4096..28672, K = 4096 and 8192 on every shape of both
+    //      kinds, e.g. N = 28672, K = 8192, M = 512 (0.875 rounds): 219.6 us against 228.0 for
+    //      256 x 256 in 2 x 4 waves (config 21, which this rule replaced: 3.6-4.4% slower on all
+    //      six shapes it took) and 241 for 128 x 256; N = 28672, K = 4096, M = 1536 (2.6 rounds):
+    //      330 vs 347; M = 4096 (7 rounds): 830 vs 847; but M = 1280 (2.2 rounds): 322 vs 290
+    //      and configs[3] (3.5 rounds): 864 vs 856 for 128 x 256;
+    //    - then, once their tiles number at least 3/4 of the CUs: 128 x 256 (two workgroups per
+    //      CU); then 128 x 128 with four waves of 128 x 32 (M >= 128), e.g. N = 28672, M = 128:
+    //      43.4 vs 55.4 us for two waves of 128 x 64, N = 4096, K = 14336, M = 1024: 137 vs 171;
+    //      then 64 x 128 with four waves of 64 x 32 (M >= 64), software-pipelined across chunks
+    //      (config 22; the unpipelined config 18 on long K), e.g. configs[2] (M = 128,
+    //      N = 14336, G = 64): 27.6 us against 30.7 for config 18 and 36.4 for token groups of
+    //      32, N = 4096, M = 512: 27.6 vs 29.2 (config 18);
     //  * token groups of 16 rows, one n16 block per wave, 4 pairs in flight, while their waves
     //    (M/16 groups x N/16 blocks) are at most 12 per CU: every small-M shape measured, e.g.
     //    K = 14336, N = 4096, M = 32: 42.8 vs 52.6 us for one wave per block over 32 rows
@@ -124,9 +133,9 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         if (wide_tiles(20) >= 0.75 * cus) return 20;
         if (group_ok(12)) return 12;
     }
-    if (M >= 256 && M <= 2048) {
-        const double t = wide_tiles(21);
-        if (t >= 0.75 * cus && t <= 2.0 * cus) return 21;
+    if (M >= 256) {
+        const double rounds = wide_tiles(23) / cus;
+        if (rounds > 0.5 && std::ceil(rounds) - rounds < 0.5) return 23;
     }
     if (wide_tiles(5) >= 0.75 * cus) return 5;
     if (M >= 128 && wide_tiles(20) >= 0.75 * cus) return 20;
@@ -350,7 +359,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
     } else {
         int cfg = v;                                          // 1..4 forced, or -1 = auto
         if (cfg < 0) {
-            if (const char* o = std::getenv("W4A16_PREFILL")) {   // tuning override: config id 1..9
+            if (const char* o = std::getenv("W4A16_PREFILL")) {   // tuning override: prefill config id
                 const int oc = std::atoi(o);
                 if (oc >= 1 && oc <= kNumPrefillTable && prefill_occupancy(oc, *lim) > 0 && prefill_shape_ok(oc, M, K)) cfg = oc;
             }

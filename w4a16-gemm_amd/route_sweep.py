@@ -26,7 +26,7 @@ from bench_gemm import LLAMA3_8B, GraphTimer, load_weights  # noqa: E402
 # Llama-3-8B projections (bench_gemm), plus BASELINE configs[2] and configs[3].
 SHAPES = [(name, n, k, 128) for name, (n, k) in LLAMA3_8B.items()] + [
     ("configs[2] gate", 14336, 4096, 64), ("configs[3] 70B gate_up", 28672, 8192, 128)]
-PREFILL_CONFIGS = range(1, 23)
+PREFILL_CONFIGS = range(1, 24)
 DECODE_VARIANTS = range(0, 32)
 DECODE_SPLITS = (1, 2, 4)
 
