@@ -71,7 +71,7 @@ typedef struct w4a16_device_limits {
 /* A launch plan: the result of validation + routing + selection.  Plain data; copyable. */
 typedef struct w4a16_plan {
     int32_t M, N, K, G;
-    int32_t kernel;           /* 0 = decode, 1..23 = prefill tile config (1..4 forced)   */
+    int32_t kernel;           /* 0 = decode, 1..24 = prefill tile config (1..4 forced)   */
     int32_t splits;           /* K ranges reduced across workgroups (decode split-K;
                                  prefill token-group configs: the K segments, K > 8192)  */
     int32_t slab_chunks;      /* decode: 64-wide K chunks per wave; prefill: chunks per

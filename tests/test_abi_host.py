@@ -125,7 +125,7 @@ def test_routing(lib, M, N, K, kernel):
     if kernel == 0:
         assert p.kernel == 0
     else:
-        assert 1 <= p.kernel <= 23
+        assert 1 <= p.kernel <= 24
 
 
 @pytest.mark.parametrize("v", [1, 2, 3, 4])
@@ -165,7 +165,8 @@ def test_prefill_plan_invariants(lib, M, N):
 PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (128, 256), 6: (256, 128), 7: (128, 128),
                  8: (32, 16), 9: (64, 16), 10: (32, 64), 11: (64, 64), 12: (32, 128), 13: (64, 128), 14: (32, 128),
                  15: (32, 256), 16: (16, 64), 17: (16, 64), 18: (64, 128), 19: (64, 256), 20: (128, 128),
-                 21: (256, 256), 22: (64, 128), 23: (128, 512)}
+                 21: (256, 256), 22: (64, 128), 23: (128, 512),
+                 24: (128, 256)}
 
 
 @pytest.mark.parametrize("M,N,K,want", [
@@ -183,8 +184,10 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (32, 28672, 4096, 10),                                                   # token groups of 32
     # long K (4 or 7 segments): split-K token groups, larger groups sooner
     (64, 4096, 14336, 10), (128, 4096, 14336, 12), (256, 4096, 14336, 13), (512, 4096, 14336, 18),
-    (17, 8192, 28672, 12), (192, 8192, 28672, 13), (384, 8192, 28672, 19), (2048, 8192, 28672, 7),
-    (2048, 4096, 14336, 7), (1024, 8192, 28672, 7),                         # long K, >= 2 rounds of 128 x 128: two 128 x 64 waves
+    (17, 8192, 28672, 12), (192, 8192, 28672, 13), (384, 8192, 28672, 19),
+    (2048, 4096, 14336, 24), (1024, 8192, 28672, 24), (2048, 8192, 28672, 24),  # long K, 128 x 256: last round > half full
+    (768, 8192, 28672, 24), (1536, 4096, 14336, 24), (512, 8192, 28672, 19), (1024, 4096, 14336, 20),
+    (3072, 4096, 14336, 7), (1536, 8192, 28672, 7),                         # long K, >= 2 rounds of 128 x 128: two 128 x 64 waves
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
@@ -196,7 +199,7 @@ def test_prefill_wide_selection(lib, M, N, K, want):
     tiles = PREFILL_TILES[p.kernel]
     assert p.grid == -(-M // tiles[0]) * -(-N // tiles[1]) * max(p.splits, 1)
     assert p.block == 64 * {1: 4, 2: 4, 3: 4, 4: 4, 5: 4, 6: 4, 7: 2, 8: 1, 9: 1, 10: 4, 11: 4, 12: 4, 13: 4, 14: 4,
-                            15: 4, 16: 4, 17: 4, 18: 4, 19: 8, 20: 4, 21: 8, 22: 4, 23: 8}[p.kernel]
+                            15: 4, 16: 4, 17: 4, 18: 4, 19: 8, 20: 4, 21: 8, 22: 4, 23: 8, 24: 8}[p.kernel]
 
 
 def test_prefill_override(lib, monkeypatch):
@@ -303,12 +306,12 @@ def test_bandwidth_probe_loads_and_rejects_bad_arguments():
 
 def test_planner_occupancy_hook_covers_every_prefill_config(lib):
     lib.w4a16_debug_prefill_occupancy.argtypes = [ctypes.c_int, ctypes.POINTER(Limits)]
-    occ = [lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(MI355X)) for cfg in range(1, 24)]
+    occ = [lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(MI355X)) for cfg in range(1, 25)]
     assert all(o >= 1 for o in occ), occ
     assert lib.w4a16_debug_prefill_occupancy(0, ctypes.byref(MI355X)) == -1
-    assert lib.w4a16_debug_prefill_occupancy(24, ctypes.byref(MI355X)) == -1
+    assert lib.w4a16_debug_prefill_occupancy(25, ctypes.byref(MI355X)) == -1
     older = Limits(256, 64 * 1024, 1024, 942)                # 64 KB of LDS per CU bounds every config
-    assert all(lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(older)) <= o for cfg, o in zip(range(1, 24), occ))
+    assert all(lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(older)) <= o for cfg, o in zip(range(1, 25), occ))
 
 
 @pytest.mark.parametrize("name,want", [
@@ -348,12 +351,12 @@ def test_long_k_plans_split_token_group_configs_by_segment(lib, monkeypatch, M, 
     s = -(-KC // 64)
     L = 2 * -(-KC // (2 * s))
     segs = -(-KC // L)
-    for cfg, kind in [(17, 3), (14, 3), (9, 2), (4, 0), (18, 1), (20, 1), (22, 1)]:
+    for cfg, kind in [(17, 3), (14, 3), (9, 2), (4, 0), (18, 1), (20, 1), (22, 1), (24, 1)]:
         monkeypatch.setenv("W4A16_PREFILL", str(cfg))
         rc, p, err = plan(lib, M=M, N=N, K=K, G=64)
         assert rc == 0, err
         if p.kernel != cfg:                        # the config does not fit this shape
-            assert cfg in (9, 4, 18, 20, 22) and (cfg != 9 or M > 64), (cfg, p.kernel)
+            assert cfg in (9, 4, 18, 20, 22, 24) and (cfg != 9 or M > 64), (cfg, p.kernel)
             continue
         bm, bn = PREFILL_TILES[cfg]
         tiles = -(-M // bm) * -(-N // bn)

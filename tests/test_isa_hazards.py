@@ -238,10 +238,10 @@ def test_wide_prefill_accumulators_stay_in_place(isa):
     copies or AGPR<->VGPR transfers (the default scheduler's allocation rotated them through
     copies, serialising the MFMA pipe)."""
     ks = {k: v for k, v in _kernels(isa).items() if "prefill_wide_kernel" in k or "prefill_wide_pipe_kernel" in k}
-    # nine configs (one of them the pipelined kernel), five of them also with the second
+    # ten configs (one of them the pipelined kernel), six of them also with the second
     # accumulator set of the long-K segments (Lb1E; checked for spills and load hazards by the
     # tests above, their loop holds the segment-close branch)
-    assert len(ks) == 14 and sum("Lb1E" in k for k in ks) == 5, list(ks)
+    assert len(ks) == 16 and sum("Lb1E" in k for k in ks) == 6, list(ks)
     for name, lines in ks.items():
         if "Lb1E" in name:
             continue

@@ -293,7 +293,8 @@ def test_wide_prefill_32x32_index_math(M, N, K, G, BM, BN, WMs, WNs):
 
 # config 22 (prefill_wide_pipe_kernel) addresses memory exactly as 18
 WIDE_TILES = {5: (128, 256, 1, 4), 6: (256, 128, 2, 2), 7: (128, 128, 1, 2), 18: (64, 128, 1, 4), 19: (64, 256, 1, 8),
-              20: (128, 128, 1, 4), 21: (256, 256, 2, 4), 22: (64, 128, 1, 4), 23: (128, 512, 1, 8)}
+              20: (128, 128, 1, 4), 21: (256, 256, 2, 4), 22: (64, 128, 1, 4), 23: (128, 512, 1, 8),
+              24: (128, 256, 1, 8)}
 
 
 @pytest.mark.parametrize("cfg", sorted(WIDE_TILES))

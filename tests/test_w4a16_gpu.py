@@ -507,11 +507,11 @@ def _onehot_decode_check(Wp, scales, Wd, K, v, splits, m):
     assert torch.equal(gemm(Wp, xo, scales, variant=0), gemm(Wp, xo, scales, variant=0))
 
 
-# Wide-tile prefill configs (5..7 and 18..23, chosen automatically for moderate and large
+# Wide-tile prefill configs (5..7 and 18..24, chosen automatically for moderate and large
 # problems; 22 is 18 software-pipelined) forced through W4A16_PREFILL:
 # bit-identical to the reference-API variants and within the reference tolerance, including M and
 # N tails (rows past M and blocks past N load clamped data and are not stored).
-@pytest.mark.parametrize("cfg", [5, 6, 7, 18, 19, 20, 21, 22, 23])
+@pytest.mark.parametrize("cfg", [5, 6, 7, 18, 19, 20, 21, 22, 23, 24])
 @pytest.mark.parametrize("M,N,K,G", [(2048, 4096, 4096, 128), (300, 1040, 2048, 64), (129, 272, 1024, 128),
                                      (17, 16, 256, 64)])
 def test_prefill_wide_configs_bitwise_equal(cfg, M, N, K, G, monkeypatch):
@@ -604,8 +604,8 @@ def test_planner_occupancy_matches_the_compiled_kernels():
     lib.w4a16_debug_prefill_occupancy.argtypes = [ctypes.c_int, ctypes.POINTER(Limits)]
     info = w4a16_opt.plan_info(2048, 4096, 4096, 128)
     lim = Limits(info["cu_count"], info["lds_bytes_per_block"], 1024, info["gcn_arch"])
-    got = {cfg: lib.w4a16_debug_kernel_occupancy(cfg) for cfg in range(1, 24)}
-    planned = {cfg: lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(lim)) for cfg in range(1, 24)}
+    got = {cfg: lib.w4a16_debug_kernel_occupancy(cfg) for cfg in range(1, 25)}
+    planned = {cfg: lib.w4a16_debug_prefill_occupancy(cfg, ctypes.byref(lim)) for cfg in range(1, 25)}
     print("compiled occupancy:", got, flush=True)
     assert got == planned
 
@@ -623,7 +623,7 @@ def test_long_k_segmented_order_bitwise_equal_across_configs(M, N, K, G, monkeyp
     want = gemm(Wp, x, scales, variant=4)
     assert_close(want, ref_gemm(x, q, scales, G, key))
     seen = []
-    for cfg in range(1, 24):
+    for cfg in range(1, 25):
         monkeypatch.setenv("W4A16_PREFILL", str(cfg))
         info = w4a16_opt.plan_info(M, N, K, G)
         if info["kernel"] != cfg:

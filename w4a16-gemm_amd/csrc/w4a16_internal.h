@@ -22,7 +22,7 @@ namespace w4a16 {
 struct PrefillTile {
     int bm, bn, waves_m, waves_n, kind, depth, wpe, occ, pipe;
 };
-constexpr PrefillTile kPrefillTable[24] = {
+constexpr PrefillTile kPrefillTable[25] = {
     {0, 0, 0, 0, 0, 0, 0, 0},
     {16, 128, 1, 4, 0, 0, 0, 7},     // 1: small batches: 4 waves across N, wave tile 16 x 32
     {32, 128, 1, 4, 0, 0, 0, 6},     // 2: wave tile 32 x 32
@@ -47,9 +47,10 @@ constexpr PrefillTile kPrefillTable[24] = {
     {256, 256, 2, 4, 1, 2, 2, 1},    // 21: wave tile 128 x 64, 2 x 4 waves (forced only)
     {64, 128, 1, 4, 1, 4, 2, 2, 1},  // 22: config 18 software-pipelined across chunks (three x buffers)
     {128, 512, 1, 8, 1, 2, 2, 1},    // 23: wave tile 128 x 64, 8 waves across N share the x rows
+    {128, 256, 1, 8, 1, 4, 2, 1},    // 24: wave tile 128 x 32, 8 waves across N share the x rows
 };
 constexpr int kNumPrefillCfg = 4;        // forced variants 1..4 (reference API)
-constexpr int kNumPrefillTable = 23;     // all prefill configs
+constexpr int kNumPrefillTable = 24;     // all prefill configs
 
 // Bytes of one LDS row (128 B of a 64-wide fp16 chunk + 16 B pad); must match kXRow.
 constexpr int kLdsRowBytes = 144;

@@ -1203,6 +1203,7 @@ W4A16_PREFILL_CFG(20)
 W4A16_PREFILL_CFG(21)
 W4A16_PREFILL_CFG(22)
 W4A16_PREFILL_CFG(23)
+W4A16_PREFILL_CFG(24)
 #undef W4A16_PREFILL_CFG
 
 template <int CFG>
@@ -1438,6 +1439,7 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
             case 21: e = launch_prefill<21>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
             case 22: e = launch_prefill<22>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
             case 23: e = launch_prefill<23>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
+            case 24: e = launch_prefill<24>(p, wp, x, scales, y, reinterpret_cast<float*>(workspace), counters, st); break;
             default: return W4A16_ERR_INVALID;
         }
     }
@@ -1475,6 +1477,7 @@ extern "C" int w4a16_debug_kernel_occupancy(int cfg) {
         case 21: return prefill_occupancy_of<21>();
         case 22: return prefill_occupancy_of<22>();
         case 23: return prefill_occupancy_of<23>();
+        case 24: return prefill_occupancy_of<24>();
         default: return -1;
     }
 }

@@ -111,10 +111,16 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     // the fastest forced config: e.g. K = 14336, N = 4096, M = 32: 19.2 us (42.8 us before the
     // segments), M = 64: 25.9 (groups of 32, one block per wave), M = 128: 38.8 (groups of 32,
     // two blocks per wave), M = 256: 58.1 (groups of 64), M = 512: 94.6 (64 x 128 wide tiles).
-    // At M >= 1024, two waves of 128 x 64 per 128 x 128 tile (config 7, one wave per SIMD) once
-    // its tiles fill two rounds of the CUs' workgroup slots (K = 14336, N = 4096, M = 2048: 237 vs
-    // 252 us for four waves of 128 x 32; K = 28672, N = 8192, M = 1024: 472 vs 499), else the four
-    // 128 x 32 waves (K = 14336, N = 4096, M = 1024: 143 vs 180 us).
+    // At M >= 512: 128 x 256 tiles of eight 128 x 32 waves sharing the x rows (config 24, one
+    // workgroup per CU) when the last round of its tiles is more than half full, as for the
+    // 128 x 512 tiles above (K = 14336, N = 4096, M = 2048: 234.5 vs 240 us for config 7,
+    // M = 1536: 191 vs 201, M = 4096: 453 vs 470; K = 28672, N = 8192, M = 768: 387 vs 493 for
+    // the 64 x 256 tiles, M = 1024: 457 vs 469, M = 2048: 912 vs 946, M = 4096: 1815 vs 1905;
+    // but M = 512 (half a round): 339 vs 283 for the 64 x 256 tiles); else two waves of 128 x 64
+    // per 128 x 128 tile (config 7, one wave per SIMD) once its tiles fill two rounds of the CUs'
+    // workgroup slots (K = 14336, N = 4096, M = 2048: 237 vs 252 us for four waves of 128 x 32;
+    // K = 28672, N = 8192, M = 1024: 472 vs 499), else the four 128 x 32 waves (K = 14336,
+    // N = 4096, M = 1024: 143 vs 180 us).
     const int segs = prefill_segments(K / 64);
     if (segs > 1) {
         auto group_waves = [&](int cfg) {
@@ -122,6 +128,10 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
             return std::ceil((double)M / t.bm) * std::ceil((double)N / t.bn) * t.waves_n * segs;
         };
         auto group_ok = [&](int cfg) { return prefill_occupancy(cfg, lim) > 0 && prefill_shape_ok(cfg, M, K); };
+        if (M >= 512) {
+            const double rounds = wide_tiles(24) / cus;
+            if (rounds > 0.5 && std::ceil(rounds) - rounds < 0.5) return 24;
+        }
         if (M >= 1024 && wide_tiles(7) >= 2.0 * cus) return 7;
         if (M >= 1024 && wide_tiles(20) >= 0.75 * cus) return 20;
         if (M >= 384 && wide_tiles(19) >= 0.75 * cus) return 19;

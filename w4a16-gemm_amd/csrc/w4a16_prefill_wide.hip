@@ -1,4 +1,4 @@
-// Wide-tile prefill (configs 5..7 and 18..23 of kPrefillTable, kind 1) in its own translation unit.
+// Wide-tile prefill (configs 5..7 and 18..24 of kPrefillTable, kind 1) in its own translation unit.
 //
 // Built with -mllvm -amdgpu-sched-strategy=max-memory-clause (build.py): with the default
 // scheduler the register allocator gives most MFMAs a destination other than their accumulator
@@ -55,8 +55,8 @@ namespace w4a16 {
 // accumulators in VGPRs and spills three registers outside the loop.  256 x 128 and 128 x 128
 // (1 x 2) stay at 1: at 2, 256 x 128 spills 67 times inside its loop and 128 x 128 spills a
 // pending asm-load destination (tests/test_isa_hazards.py rejects that).  The 32-channel wave
-// tiles (configs 18..20) and the 8-wave tiles of 128 x 64 waves (256 x 256 and 128 x 512) fit 2
-// without spills.
+// tiles (configs 18..20, 24) and the 8-wave tiles of 128 x 64 waves (256 x 256 and 128 x 512) fit
+// 2 without spills.
 // SEG: K longer than one canonical segment (seg_chunks chunks, even): acc holds the running
 // segment and total the sum of the finished ones (total = p0, then total + p_s), closed after
 // every seg_chunks chunks of the two-chunk loop.
@@ -617,6 +617,7 @@ hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const
         case 21: return launch_wide<21>(p, Wp, x, s, y, st);
         case 22: return launch_wide<22>(p, Wp, x, s, y, st);
         case 23: return launch_wide<23>(p, Wp, x, s, y, st);
+        case 24: return launch_wide<24>(p, Wp, x, s, y, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -649,6 +650,7 @@ int prefill_wide_occupancy(int cfg) {
         case 21: return occupancy_wide<21>();
         case 22: return occupancy_wide<22>();
         case 23: return occupancy_wide<23>();
+        case 24: return occupancy_wide<24>();
         default: return -1;
     }
 }

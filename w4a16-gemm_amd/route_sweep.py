@@ -5,9 +5,9 @@ For each (N, K, G) shape and M, times `w4a16_gemm(Wp, x, scales)` with the auto 
 each prefill tile config forced through W4A16_PREFILL (M > 16) or each decode kernel shape and
 split count forced through W4A16_DECODE (M <= 16), and reports the auto config, the fastest
 forced config and their ratio.  Timing is bench_gemm's: a HIP graph of calls over distinct weight
-copies (working set --target-mb), median per call over --reps replays, the faster of two rounds
-(auto first in one, last in the other).  A forced setting the planner ignores (the config does
-not fit the shape) is skipped.
+copies (working set --target-mb), replayed untimed for --warm-ms first, median per call over
+--reps replays, the faster of two rounds (auto first in one, last in the other).  A forced
+setting the planner ignores (the config does not fit the shape) is skipped.
 
     python w4a16-gemm_amd/route_sweep.py --md out.md
 """
@@ -16,6 +16,7 @@ from __future__ import annotations
 import argparse
 import os
 import sys
+import time
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 if HERE not in sys.path:
@@ -26,9 +27,23 @@ from bench_gemm import LLAMA3_8B, GraphTimer, load_weights  # noqa: E402
 # Llama-3-8B projections (bench_gemm), plus BASELINE configs[2] and configs[3].
 SHAPES = [(name, n, k, 128) for name, (n, k) in LLAMA3_8B.items()] + [
     ("configs[2] gate", 14336, 4096, 64), ("configs[3] 70B gate_up", 28672, 8192, 128)]
-PREFILL_CONFIGS = range(1, 24)
+PREFILL_CONFIGS = range(1, 25)
 DECODE_VARIANTS = range(0, 32)
 DECODE_SPLITS = (1, 2, 4)
+
+
+def settled_timer(torch, calls, warm_ms: float):
+    """bench_gemm's GraphTimer, replayed untimed for at least warm_ms of wall time first: the
+    shader clock of a power-bound launch takes tens of milliseconds to settle after the GPU idles
+    (graph capture, a switch of shapes), and a few warm replays leave a setting timed early in that
+    ramp reading several percent high."""
+    timer = GraphTimer(torch, calls)
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(4):
+            timer.graph.replay()
+        torch.cuda.synchronize()
+    return timer
 
 
 def forced_plans(w4a16_opt, M, N, K, G):
@@ -58,6 +73,7 @@ def main(argv=None) -> int:
     ap.add_argument("--shape", action="append", help="name,N,K,G (repeatable); default: Llama-3-8B + configs[2..3]")
     ap.add_argument("--target-mb", type=float, default=512)
     ap.add_argument("--reps", type=int, default=10)
+    ap.add_argument("--warm-ms", type=float, default=30.0, help="untimed replays before each timing (ms of wall time)")
     ap.add_argument("--md", default=None, help="write the summary table (Markdown) here")
     ap.add_argument("--json", default=None, help="write every timing (auto and each forced setting) here")
     args = ap.parse_args(argv)
@@ -86,13 +102,13 @@ def main(argv=None) -> int:
             for order in (["auto"] + forced, forced + ["auto"]):
                 for item in order:
                     if item == "auto":
-                        us = GraphTimer(torch, calls).per_call_us(args.reps)[0]
+                        us = settled_timer(torch, calls, args.warm_ms).per_call_us(args.reps)[0]
                         times["auto"] = min(times.get("auto", us), us)
                         continue
                     label, var, value, kname = item
                     os.environ[var] = value
                     try:
-                        us = GraphTimer(torch, calls).per_call_us(args.reps)[0]
+                        us = settled_timer(torch, calls, args.warm_ms).per_call_us(args.reps)[0]
                     finally:
                         del os.environ[var]
                     times[label] = min(times.get(label, us), us)
