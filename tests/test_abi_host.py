@@ -171,7 +171,8 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
 
 @pytest.mark.parametrize("M,N,K,want", [
     (2048, 28672, 8192, 5), (1280, 28672, 4096, 5), (4096, 6144, 4096, 5),   # 128x512 last round half full or less
-    (1024, 6144, 4096, 5),                                                   # >= 3/4 of the CUs: 128x256
+    (1024, 6144, 4096, 24), (512, 14336, 4096, 24), (2048, 4096, 4096, 24),  # one round of 128x256 8-wave tiles
+    (256, 28672, 8192, 24),
     (2048, 14336, 4096, 23), (512, 28672, 8192, 23), (2048, 6144, 4096, 23), # 128x512: last round > half full
     (1024, 28672, 8192, 23), (4096, 4096, 4096, 23), (1536, 28672, 4096, 23), (768, 14336, 4096, 23),
     (768, 28672, 4096, 5),

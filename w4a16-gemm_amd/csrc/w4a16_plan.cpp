@@ -86,6 +86,12 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //      six shapes it took) and 241 for 128 x 256; N = 28672, K = 4096, M = 1536 (2.6 rounds):
     //      330 vs 347; M = 4096 (7 rounds): 830 vs 847; but M = 1280 (2.2 rounds): 322 vs 290
     //      and configs[3] (3.5 rounds): 864 vs 856 for 128 x 256;
+    //    - 128 x 256 tiles of eight 128 x 32 waves sharing the x rows (config 24, one workgroup
+    //      per CU) when they make one round more than half full, e.g. BASELINE configs[2]'s shape
+    //      at M = 512: 64.1 vs 69.9 us for 128 x 256 tiles two per CU, N = 4096, K = 4096,
+    //      M = 2048: 69.5 vs 73.8, N = 28672, K = 8192, M = 256: 124.1 vs 129.5; over several
+    //      rounds the 128 x 32 wave tiles lose to the 128 x 64 ones (N = 28672, M = 2048: 465 vs
+    //      425 at K = 4096);
     //    - then, once their tiles number at least 3/4 of the CUs: 128 x 256 (two workgroups per
     //      CU); then 128 x 128 with four waves of 128 x 32 (M >= 128), e.g. N = 28672, M = 128:
     //      43.4 vs 55.4 us for two waves of 128 x 64, N = 4096, K = 14336, M = 1024: 137 vs 171;
@@ -146,6 +152,8 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     if (M >= 256) {
         const double rounds = wide_tiles(23) / cus;
         if (rounds > 0.5 && std::ceil(rounds) - rounds < 0.5) return 23;
+        const double rounds24 = wide_tiles(24) / cus;
+        if (rounds24 > 0.5 && rounds24 <= 1.0) return 24;
     }
     if (wide_tiles(5) >= 0.75 * cus) return 5;
     if (M >= 128 && wide_tiles(20) >= 0.75 * cus) return 20;
