@@ -346,8 +346,11 @@ def ring_x_rows(x, M, K, c0, XR):
     pair of fp64 halves).  XR == 1: one 4-byte load, lane j fetching dword 32*(u/8) + 16*((u/4)%2)
     + 4*(j%4) + u%4 of the pair (u = j / 4).  XR >= 4: 16-byte loads of 4 rows each, lane j of
     load q filling row (64q + j) / 16, segment j % 16 with global segment (j % 16) ^ (row % 8).
-    Also returns the largest source byte offset touched within an x row."""
+    Also returns the largest source byte offset touched within an x row and, for XR >= 4, the
+    slot's LDS bytes as the loads write them (byte offset -> dword; rows 8..15 of a 16-row slot
+    start 8 bytes further on)."""
     slot = np.empty((XR, 64, 2))
+    phys = {}
     hi = 0
     if XR == 1:
         for lane in range(64):
@@ -356,16 +359,18 @@ def ring_x_rows(x, M, K, c0, XR):
             off = c0 * 128 + 4 * d
             hi = max(hi, off + 4)
             slot[0, lane] = x[0, off // 2:off // 2 + 2]
-        return slot, hi
+        return slot, hi, phys
     for q in range(XR // 4):
         for lane in range(64):
             r = (64 * q + lane) >> 4
             gseg = (lane & 15) ^ (r & 7)
             off = c0 * 128 + gseg * 16
             hi = max(hi, off + 16)
+            dst = q * 1024 + (8 if XR == 16 and q >= 2 else 0) + lane * 16     # the DMA's LDS bytes
             for e in range(4):
                 slot[r, 4 * (lane & 15) + e] = x[min(r, M - 1), off // 2 + 2 * e:off // 2 + 2 * e + 2]
-    return slot, hi
+                phys[dst + 4 * e] = tuple(slot[r, 4 * (lane & 15) + e])
+    return slot, hi, phys
 
 
 def ring_b_operand(slot, M, XR, cc, h):
@@ -384,9 +389,9 @@ def ring_b_operand(slot, M, XR, cc, h):
             for c in range(4):
                 pos = 8 * cc + ((4 * h + c) ^ (xr & 7))
                 dws.append(slot[xr, 4 * pos + kb])
-                if c == 0:
-                    addr.append(xr * 256 + pos * 16 + 4 * kb)
             B[lane] = np.concatenate(dws)
+            addr.append([xr * 256 + (8 if XR == 16 and xr >= 8 else 0) + (8 * cc + ((4 * h + c) ^ (xr & 7))) * 16 + 4 * kb
+                         for c in range(4)])
     return B, addr
 
 
@@ -400,8 +405,11 @@ def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
     loads plus four 4-byte LDS reads otherwise), the waves of a workgroup interleaved over K (wave w
     takes chunk pairs w, w + WAVES, ...), the weights as in decode_kernel: the emulated
     result equals the float64 matmul, every x source offset stays inside the row, every B operand
-    holds x[row][32h + 8c + 2kb + {0,1}] in slot pair c, and the first-dword reads of 8 consecutive
-    lanes with 8 distinct rows hit 8 distinct 16-byte bank groups."""
+    holds x[row][32h + 8c + 2kb + {0,1}] in slot pair c, the first-dword reads of 8 consecutive
+    lanes with 8 distinct rows hit 8 distinct 16-byte bank groups, and with 16 distinct rows
+    (rows 8..15 8 bytes further on) every 4-byte read hits 32 distinct banks in each half-wave (the
+    LDS serves a 4-byte read 32 lanes at a time from 32 banks, measured: 0 conflict cycles at
+    M <= 8, two per read at M = 16 without the shift)."""
     rng = np.random.default_rng(M * 11 + K)
     q = rng.integers(0, 16, (N, K), dtype=np.uint8)
     s = rng.random((K // G, N)) * 0.05 + 0.001
@@ -420,7 +428,7 @@ def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
                 acc = np.zeros((NBW, 64, 4))
                 for p in range(kcw // 2):
                     c0 = kc0 + 2 * WAVES * p
-                    slot, hi = ring_x_rows(x, M, K, c0, XR)
+                    slot, hi, phys = ring_x_rows(x, M, K, c0, XR)
                     assert hi <= 2 * K
                     for cc in range(2):
                         Bs = []
@@ -431,10 +439,18 @@ def test_ring_decode_x_rows_index_math(M, N, K, G, NBW, WAVES, splits):
                                 base = (c0 + cc) * 64 + 32 * h + 2 * kb
                                 want = [x[min(j, M - 1), base + 8 * c + e] for c in range(4) for e in range(2)]
                                 assert np.array_equal(B[lane], want)
-                            for g0 in range(0, 64, 8):
-                                rows = {min(j, M - 1) for j in range(g0 & 15, (g0 & 15) + 8)}
-                                if len(rows) == 8:
-                                    assert len({a // 16 % 8 for a in addr[g0:g0 + 8]}) == 8
+                            if XR > 1:
+                                for g0 in range(0, 64, 8):
+                                    rows = {min(j, M - 1) for j in range(g0 & 15, (g0 & 15) + 8)}
+                                    if len(rows) == 8:
+                                        assert len({a[0] // 16 % 8 for a in addr[g0:g0 + 8]}) == 8
+                                for lane in range(64):      # the read addresses find the loaded dwords
+                                    for c in range(4):
+                                        assert phys[addr[lane][c]] == tuple(B[lane, 2 * c:2 * c + 2])
+                                if M >= 16:                 # 16 distinct rows: each half-wave on 32 distinct banks
+                                    for c in range(4):
+                                        for half in (addr[:32], addr[32:]):
+                                            assert len({a[c] // 4 % 32 for a in half}) == 32, (cc, h, c)
                             Bs.append(B)
                         kc = c0 + cc
                         for b in range(NBW):
@@ -458,13 +474,13 @@ def group_x_slot(x, M, K, m0, c0, TM):
     """prefill_group_kernel x rows of one chunk pair (chunks c0, c0+1) as they land in LDS:
     a dict byte offset -> fp64 half pair (one dword), for TM tiles of 16 token rows.  16-byte
     direct-to-LDS load q (4 rows) writes rows r0 = 4 (q % 4) .. r0 + 3 of tile t = q // 4 at
-    t * 4352 + r0 * 256 + 128 * (r0 >= 8); lane j writes row r0 + j // 16, position j % 16, with
+    t * 4352 + r0 * 256 + 8 * (r0 >= 8); lane j writes row r0 + j // 16, position j % 16, with
     global segment (j % 16) ^ (row % 8) of token min(m0 + 16 t + row, M - 1)."""
     lds = {}
     hi = 0
     for q in range(4 * TM):
         t, r0 = q // 4, 4 * (q % 4)
-        base = t * 4352 + r0 * 256 + (128 if r0 >= 8 else 0)
+        base = t * 4352 + r0 * 256 + (8 if r0 >= 8 else 0)
         for lane in range(64):
             r = r0 + (lane >> 4)
             g = (lane & 15) ^ (r & 7)
@@ -479,10 +495,10 @@ def group_x_slot(x, M, K, m0, c0, TM):
 @pytest.mark.parametrize("M,TM", [(17, 2), (64, 4), (100, 4), (16, 1)])
 def test_group_prefill_x_rows_b_operand(M, TM):
     """prefill_group_kernel B operands without cross-lane transposes: lane (kb, li) of token tile
-    t, chunk cc, half h reads four dwords at t*4352 + li*256 + 128*(li >= 8) +
+    t, chunk cc, half h reads four dwords at t*4352 + li*256 + 8*(li >= 8) +
     (8 cc + ((4h + c) ^ (li % 8))) * 16 + 4 kb (c = 0..3); they must hold x[token][32h + 8c + 2kb
     + {0,1}] of chunk cc, every x source offset stays inside the row, and for every (t, cc, h, c)
-    the 64 lanes hit 64 distinct 4-byte banks (16 distinct rows, no conflicts)."""
+    each half-wave (32 lanes, served together from 32 banks) hits 32 distinct 4-byte banks."""
     rng = np.random.default_rng(M)
     K = 512
     x = rng.standard_normal((M, K))
@@ -494,15 +510,15 @@ def test_group_prefill_x_rows_b_operand(M, TM):
                 for cc in range(2):
                     for h in range(2):
                         for c in range(4):
-                            banks = set()
+                            banks = [set(), set()]
                             for lane in range(64):
                                 kb, li = lane >> 4, lane & 15
-                                a = t * 4352 + li * 256 + (128 if li >= 8 else 0) + (8 * cc + ((4 * h + c) ^ (li & 7))) * 16 + 4 * kb
-                                banks.add(a // 4 % 64)
+                                a = t * 4352 + li * 256 + (8 if li >= 8 else 0) + (8 * cc + ((4 * h + c) ^ (li & 7))) * 16 + 4 * kb
+                                banks[lane >> 5].add(a // 4 % 32)
                                 tok = min(m0 + 16 * t + li, M - 1)
                                 k = (c0 + cc) * 64 + 32 * h + 8 * c + 2 * kb
                                 assert lds[a] == (x[tok, k], x[tok, k + 1])
-                            assert len(banks) == 64
+                            assert len(banks[0]) == 32 and len(banks[1]) == 32
 
 
 @pytest.mark.parametrize("tiles_m,tiles_n", [(16, 112), (16, 24), (3, 5), (1, 7), (5, 1), (9, 13), (16, 16)])

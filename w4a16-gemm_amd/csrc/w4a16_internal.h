@@ -56,7 +56,7 @@ constexpr int kNumPrefillTable = 24;     // all prefill configs
 constexpr int kLdsRowBytes = 144;
 
 // Bytes of one 16-row token tile in a prefill_group_kernel slot: 16 rows x 256 B, rows 8..15
-// shifted by 128 B (bank spread), rounded up to a multiple of 128.
+// shifted by 8 B (bank spread), rounded up to a multiple of 256.
 constexpr int kGroupXTileBytes = 16 * 256 + 256;
 
 // Ring slot of kinds 2 and 3: kind 2 per wave 1 KB of weights and 1 KB of scales, plus the x rows
@@ -157,7 +157,8 @@ constexpr int decode_lds_bytes(int v, int M) {
     return kDecodeTable[v].kind == 0   ? kDecodeTable[v].waves * kDecodeTable[v].nbw * 64 * 16 + 16
            : kDecodeTable[v].kind == 2 ? kDecodeTable[v].waves * kDecodeTable[v].nbw * kDecodeTable[v].d * 1024 + 16
                                        : kDecodeTable[v].waves * (kDecodeTable[v].d + 1) *
-                                             (kDecodeTable[v].nbw * 1088 + decode_ring_xr(M) * 256) + 16;
+                                             (kDecodeTable[v].nbw * 1088 + decode_ring_xr(M) * 256 +
+                                              (decode_ring_xr(M) == 16 ? 16 : 0)) + 16;
 }
 // Whether a decode shape can cover K (in 64-wide chunks, group size G) with `splits` workgroups
 // per column tile.

@@ -415,7 +415,11 @@ decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 //    dwords 16h + 4c + kb (c = 0..3) of row j's chunk, a stride-4 gather:
 //      - XR >= 4 (M >= 2): 16-byte loads of 4 rows each (XR/4 per pair), 16-byte segments
 //        XOR-swizzled by row; the B operand is four 4-byte LDS reads from the swizzled segments
-//        (the reads of 8 distinct rows hit distinct banks);
+//        (a 4-byte read is served 32 lanes at a time from 32 banks: lanes (kb, j) with kb = 0, 1
+//        use dwords 0, 1 of their rows' segments; the reads of 8 distinct rows hit distinct banks,
+//        and with 16 rows, rows 8..15 sit 8 bytes further on, so they use the segments' dwords
+//        2, 3 and the 32 lanes hit 32 distinct banks; unshifted, rows r and r + 8 shared a bank
+//        and every such read cost two extra cycles, 0.46-0.92 M conflict cycles per launch);
 //      - XR == 1 (M == 1): one 4-byte load per pair in which each lane picks the dword it
 //        fetches so that the row lands already in B-operand order (16-byte unit 8cc + 4h + kb
 //        holds dwords 16h + 4c + kb of chunk cc); the B operand is one 16-byte LDS read and the
@@ -442,7 +446,8 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                    int M, int N, int K, int gshift, int splits, int kcw) {
     constexpr int S = D + 1;                                 // ring slots
     constexpr int WSLOT = NBW * 1024;                        // [n16 block][chunk][32 x 16 B]
-    constexpr int XSLOT = XR * 256;                          // [XR rows][16 x 16 B]
+    constexpr int XHI = XR == 16 ? 8 : 0;                    // shift of rows 8..15 (bank spread)
+    constexpr int XSLOT = XR * 256 + (XHI ? 16 : 0);         // [XR rows][16 x 16 B], 16-byte aligned
     constexpr int SCOFF = WSLOT + XSLOT;                     // [chunk][block][16 halves]
     constexpr int SLOT = SCOFF + 64 * NBW;
     constexpr int WAVE_BYTES = S * SLOT;
@@ -482,9 +487,10 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // Ring load sources: a base that advances per pair plus a fixed per-lane byte offset.
     // Weights: lane j fills segment j & 31 of chunk j >> 5 with packed lane 4*(seg % 8) + seg / 8.
     // x, XR >= 4: lane j of load q fills row r = (64q + j) / 16, segment j % 16, with global
-    // segment (j % 16) ^ (r % 8) of row min(r, M - 1).  x, XR == 1: lane j fills dword j of the
-    // row's 256 bytes, i.e. dword e = j % 4 of unit u = j / 4 (chunk u / 8, half (u / 4) % 2,
-    // lane group u % 4), so it fetches dword 32*(u/8) + 16*((u/4)%2) + 4e + u%4 of the row's pair.
+    // segment (j % 16) ^ (r % 8) of row min(r, M - 1); rows 8..15 start XHI bytes later.
+    // x, XR == 1: lane j fills dword j of the row's 256 bytes, i.e. dword e = j % 4 of unit
+    // u = j / 4 (chunk u / 8, half (u / 4) % 2, lane group u % 4), so it fetches dword
+    // 32*(u/8) + 16*((u/4)%2) + 4e + u%4 of the row's pair.
     const int wseg = lane & 31;
     const uint32_t woff_g = (uint32_t)((((lane >> 5) * 32) + 4 * (wseg & 7) + (wseg >> 3)) * 16);
     const char* wbase_g = reinterpret_cast<const char*>(Wp) + ((size_t)nb0 * KC + kc0) * 512;
@@ -521,7 +527,9 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
             for (int q = 0; q < XD; ++q)
                 __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * (256 * WAVES)),
-                                                 (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024), 16, 0, 0);
+                                                 (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024 +
+                                                                                           (q >= 2 ? XHI : 0)),
+                                                 16, 0, 0);
         }
         if (lane < 4 * NBW)
             __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)p * (sstep * WAVES)),
@@ -542,7 +550,7 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         } else {
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                xb[h][c] = lds_wave + WSLOT + xr * 256 + (((4 * h + c) ^ (xr & 7)) << 4) + 4 * kb;
+                xb[h][c] = lds_wave + WSLOT + xr * 256 + (xr >= 8 ? XHI : 0) + (((4 * h + c) ^ (xr & 7)) << 4) + 4 * kb;
         }
     }
     const uint32_t wb = lds_wave + (((li & 7) + 8 * kb) << 4);
@@ -963,9 +971,11 @@ prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 // the last block (clamped) and not stored.
 //
 // x layout in a slot: token tile t (16 rows) at t * XT; row r at r * 256, rows 8..15 shifted by
-// 128 bytes; the 16-byte global segment g of a row sits at position g ^ (r % 8).  The B operand
+// 8 bytes; the 16-byte global segment g of a row sits at position g ^ (r % 8).  The B operand
 // of lane (kb, j) -- dwords 16h + 4c + kb (c = 0..3) of row j's chunk cc -- is read as four 4-byte
-// LDS reads, with no cross-lane transpose.  Per wave, a slot holds NB KB of weights and the
+// LDS reads, with no cross-lane transpose.  The LDS serves a 4-byte read 32 lanes at a time from
+// 32 banks; lanes kb = 0, 1 (or 2, 3) read dwords kb of their rows' segments, and the 8-byte
+// shift moves rows 8..15 onto the segments' other two dwords, so the 32 lanes hit 32 banks.  Per wave, a slot holds NB KB of weights and the
 // pair's scales ([block][chunk][16 channels], 64 B per block).  The ring loop is unrolled by its
 // size, so every LDS offset is an instruction immediate.
 template <int TM, int D, int W, int NB>
@@ -1045,7 +1055,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             const int r0 = 4 * (q & 3);
             __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + (size_t)p * 128),
                                              (__attribute__((address_space(3))) void*)(sl + XOFF + (q >> 2) * XT + r0 * 256 +
-                                                                                       (r0 >= 8 ? 128 : 0)),
+                                                                                       (r0 >= 8 ? 8 : 0)),
                                              16, 0, 0);
         }
         if (lane < 4 * NB)
@@ -1061,7 +1071,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            xb[h][c] = lds + XOFF + li * 256 + (li >> 3) * 128 + (((4 * h + c) ^ (li & 7)) << 4) + 4 * kb;
+            xb[h][c] = lds + XOFF + li * 256 + (li >> 3) * 8 + (((4 * h + c) ^ (li & 7)) << 4) + 4 * kb;
     const uint32_t wb = lds + wave * WR + (((li & 7) + 8 * kb) << 4);
     const uint32_t sb = lds + wave * WR + NB * 1024 + (li >> 3) * 16 + (li & 7) * 2;   // + 64 block + 32 chunk
     const Dq d = dq_setup(lane);
