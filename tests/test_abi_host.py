@@ -181,7 +181,7 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (128, 14336, 4096, 22), (512, 4096, 4096, 22), (64, 28672, 4096, 22),    # 64x128, four 64x32 waves, pipelined
     (2048, 28672, 8256, None),                                               # odd chunk count: classic only
     (17, 4096, 14336, 17), (32, 6144, 4096, 17), (32, 14336, 4096, 17),     # token groups of 16
-    (33, 4096, 4096, 17), (64, 4096, 4096, 17), (48, 14336, 4096, 17), (128, 6144, 4096, 17),
+    (33, 4096, 4096, 17), (64, 4096, 4096, 17), (48, 14336, 4096, 10), (128, 6144, 4096, 10),
     (32, 28672, 4096, 10),                                                   # token groups of 32
     # long K (4 or 7 segments): split-K token groups, larger groups sooner
     (64, 4096, 14336, 10), (128, 4096, 14336, 12), (256, 4096, 14336, 13), (512, 4096, 14336, 18),

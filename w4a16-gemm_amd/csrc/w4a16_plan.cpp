@@ -100,9 +100,10 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     //      N = 14336, G = 64): 27.6 us against 30.7 for config 18 and 36.4 for token groups of
     //      32, N = 4096, M = 512: 27.6 vs 29.2 (config 18);
     //  * token groups of 16 rows, one n16 block per wave, 4 pairs in flight, while their waves
-    //    (M/16 groups x N/16 blocks) are at most 12 per CU: every small-M shape measured, e.g.
+    //    (M/16 groups x N/16 blocks) are at most 8 per CU: every small-M shape measured, e.g.
     //    K = 14336, N = 4096, M = 32: 42.8 vs 52.6 us for one wave per block over 32 rows
-    //    (prefill_stream_kernel, now forced-only);
+    //    (prefill_stream_kernel, now forced-only); at 12 per CU token groups of 32 rows are
+    //    faster (N = 6144, M = 128: 19.0 vs 21.3 us);
     //  * token groups of 32 rows with two n16 blocks per wave (every x operand read feeds two
     //    MFMAs) while their waves (M/32 groups x N/32 block pairs) number 4..12 per CU, 3 pairs
     //    in flight up to 8 per CU, else 2;
@@ -160,7 +161,7 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     if (M >= 64 && wide_tiles(22) >= 0.75 * cus) return 22;
     const double blocks = std::ceil(N / 16.0);
     if (prefill_occupancy(17, lim) > 0 && prefill_shape_ok(17, M, K) &&
-        std::ceil(M / 16.0) * blocks <= 12.0 * cus)
+        std::ceil(M / 16.0) * blocks <= 8.0 * cus)
         return 17;
     const double waves2 = std::ceil(M / 32.0) * std::ceil(N / 32.0);
     if (waves2 >= 4.0 * cus && waves2 <= 12.0 * cus) {
