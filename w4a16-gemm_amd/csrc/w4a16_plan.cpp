@@ -283,8 +283,8 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             // w4a16-gemm_amd/route_sweep.py) for the Llama-3 decode projections, tried in order;
             // the first that fits wins:
             //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): refill-ahead
-            //    rings of 4 waves, 2 blocks while the x rows are few (M <= 4), else 4 blocks; no
-            //    split.  Twice as wide (fused gate/up, N = 28672): single-block rings of 8 waves
+            //    rings of 4 waves, 2 blocks while the x rows are few (M <= 8: M = 8, 9.51 vs
+            //    9.88 us), else 4 blocks (M = 16: 10.05 vs 11.16 us); no split.  Twice as wide (fused gate/up, N = 28672): single-block rings of 8 waves
             //    at M = 1 (14.6 vs 16.8 us), of 4 waves with 4 pairs in flight at M <= 4;
             //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves,
             //    3 pairs in flight up to 4 token rows and 2 up to 8 rows; above 8 rows, where the x
@@ -327,8 +327,10 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             const int n = 3;
             const bool very_wide = (int64_t)ntiles_of(12) * 2 >= 3LL * cus;
             const bool many_blocks = N / 16 > cus;                      // single-block tiles: over one per CU
-            if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus)
-                list = M <= 1 && very_wide ? vwide_m1 : M <= 4 ? (very_wide ? vwide_small_m : wide_small_m) : wide;
+            if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus && very_wide)
+                list = M <= 1 ? vwide_m1 : M <= 4 ? vwide_small_m : wide;
+            else if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus)
+                list = M <= 8 ? wide_small_m : wide;
             else if (KC >= 128 && many_blocks)
                 list = M <= 1 ? many_m1 : M <= 4 ? many_longk_m4 : M <= 8 ? many_small_m : many_longk_large_m;
             else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
