@@ -23,9 +23,11 @@ as the JSON line.
 Algorithmic work (the roofline numerator): bytes = N*K/2 + (K/G)*N*2 + M*K*2 + M*N*2 per call,
 flops = 2*M*N*K per call.  Peaks: HBM 8000 GB/s, fp16 dense MFMA 2500 TFLOP/s (MI355X spec).
 
-The CPU baseline times the oracle's C restatement of the reference CPU path (unpack + fp16
-dequant + fp32 GEMM, oracle/w4a16_oracle.c) on the host on a bounded sample of the same cases.
-Prints ONE JSON line.
+The CPU baseline times the reference CPU path (unpack + fp16 (q-8)*s dequant, then the fp32
+torch matmul and the fp16 cast: tests/quant.py:51-59, 77-85, restated in oracle/torch_ref.py) on
+torch-CPU with every host thread, median of 5 reps per case (2 for configs[3], on a column slice),
+with the dequant / matmul split and the CPU model in the JSON.  The baseline GEMV leg times the
+oracle's C reference-order GEMV.  Prints ONE JSON line.
 """
 from __future__ import annotations
 
