@@ -98,7 +98,11 @@ int w4a16_plan_create(const w4a16_problem* prob, int variant, const w4a16_device
  *               It must be all-zero before the first launch that uses it; every launch leaves
  *               it all-zero again.  Launches that share one counter buffer must not overlap
  *               in time (use one buffer per concurrently running stream).
- * Returns W4A16_OK or W4A16_ERR_HIP / W4A16_ERR_WORKSPACE. */
+ * The plan is checked against what its kernel derives from (M, N, K, G) before anything is
+ * launched: a plan that does not match (grid, chunks per wave, block, shape id, split count)
+ * returns W4A16_ERR_INVALID, a split plan whose buffers are declared too small
+ * W4A16_ERR_WORKSPACE.
+ * Returns W4A16_OK, W4A16_ERR_INVALID, W4A16_ERR_WORKSPACE or W4A16_ERR_HIP. */
 int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
                  const uint16_t* scales, uint16_t* y, void* workspace, int32_t* counters,
                  void* stream);

@@ -1,5 +1,6 @@
 """CPU tests of the C ABI (include/w4a16.h) of libw4a16_hip.so: exports, validation, routing,
-planning.  Only pure host entry points are called (no device work), so these run without a GPU.
+planning.  Only pure host entry points are called (no device work), plus w4a16_launch with plans
+it refuses before any HIP call, so these run without a GPU.
 
 The validation order and messages mirror the reference op (src/vectorized/kernel.cu:219-249) and
 the substrings its tests match (tests/test_w4a16.py:188-195, 281-305).
@@ -386,3 +387,45 @@ def test_canonical_segments():
     for KC in range(129, 5000):
         L, S = segs(KC)
         assert L % 2 == 0 and L <= 64 + 1 and 0 < KC - (S - 1) * L <= L
+
+
+def _launch(lib, p, workspace=16, counters=16):
+    """w4a16_launch with dummy pointers that are never dereferenced: a plan that fails the
+    launch-side check returns before any HIP call, so this runs without a GPU."""
+    lib.w4a16_launch.argtypes = [ctypes.POINTER(Plan)] + [ctypes.c_void_p] * 7
+    lib.w4a16_launch.restype = ctypes.c_int
+    return lib.w4a16_launch(ctypes.byref(p), 16, 16, 16, 16, workspace, counters, None)
+
+
+@pytest.mark.parametrize("field,delta", [("grid", 1), ("grid", -1), ("slab_chunks", 1), ("slab_chunks", -1),
+                                          ("block", 64), ("decode_variant", 40), ("splits", 1), ("M", 16),
+                                          ("N", 48), ("K", 512), ("G", 64)])
+def test_launch_rejects_decode_plan_not_matching_its_shape(lib, field, delta):
+    """A decode plan whose grid, chunks per wave, block, shape id, split count or shape disagree
+    is refused (W4A16_ERR_INVALID) before anything is launched: the kernels index the weights,
+    x and y by the plan, so a stale or edited plan must not reach them."""
+    for M, N, K in [(1, 14336, 4096), (8, 4096, 14336), (16, 4096, 14336)]:
+        rc, p, err = plan(lib, M=M, N=N, K=K, G=128)
+        assert rc == 0 and p.kernel == 0, err
+        setattr(p, field, getattr(p, field) + delta)
+        assert _launch(lib, p) == 1, (M, N, K, field)
+
+
+def test_launch_checks_split_buffers_of_decode_plans(lib):
+    rc, p, err = plan(lib, M=16, N=4096, K=14336, G=128)
+    assert rc == 0 and p.kernel == 0 and p.splits == 2, (err, p.splits)
+    for field in ("workspace_bytes", "counter_slots"):
+        q = Plan.from_buffer_copy(p)
+        setattr(q, field, getattr(q, field) - 1)
+        assert _launch(lib, q) == 4, field                      # W4A16_ERR_WORKSPACE
+    assert _launch(lib, Plan.from_buffer_copy(p), workspace=None) == 4
+    assert _launch(lib, Plan.from_buffer_copy(p), counters=None) == 4
+
+
+def test_launch_rejects_prefill_plan_not_matching_its_shape(lib):
+    rc, p, err = plan(lib, M=300, N=4096, K=4096, G=64)
+    assert rc == 0 and p.kernel >= 1, err
+    for field, delta in (("grid", 1), ("kernel", 100), ("G", 32)):
+        q = Plan.from_buffer_copy(p)
+        setattr(q, field, getattr(q, field) + delta)
+        assert _launch(lib, q) == 1, field

@@ -1404,7 +1404,23 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
     if (p.grid <= 0 || p.M <= 0 || p.N <= 0 || p.K <= 0) return W4A16_OK;   // empty output
     if (p.workspace_bytes && !workspace) return W4A16_ERR_WORKSPACE;
     if (p.counter_slots && !counters) return W4A16_ERR_WORKSPACE;
-    if (p.kernel >= 1 && p.kernel <= kNumPrefillTable) {
+    if ((p.G != 64 && p.G != 128) || p.K % 64 != 0 || p.N % 16 != 0 || p.K % p.G != 0) return W4A16_ERR_INVALID;
+    if (p.kernel == W4A16_VARIANT_DECODE) {
+        // A decode plan must match what its shape id derives from (M, N, K): the grid, the
+        // chunks per wave and the block size bound every weight, x and y index its kernel forms.
+        if (p.decode_variant < 0 || p.decode_variant >= kNumDecodeCfg) return W4A16_ERR_INVALID;
+        const DecodeCfg& c = kDecodeTable[p.decode_variant];
+        const int KC = p.K >> 6;
+        const int ntiles = p.N / (16 * c.nbw);
+        if (p.M > 16 || p.N % 64 != 0 || p.K % 512 != 0 || p.N % (16 * c.nbw) != 0 ||
+            !decode_shape_fits(p.decode_variant, KC, p.splits, p.G) ||
+            p.slab_chunks != KC / (p.splits * c.waves) || p.block != c.waves * 64 ||
+            (int64_t)p.grid != (int64_t)ntiles * p.splits)
+            return W4A16_ERR_INVALID;
+        if (p.splits > 1 && (p.counter_slots < ntiles ||
+                             p.workspace_bytes < (uint64_t)p.splits * p.M * p.N * sizeof(float)))
+            return W4A16_ERR_WORKSPACE;
+    } else if (p.kernel >= 1 && p.kernel <= kNumPrefillTable) {
         // A prefill plan must match what its kernel derives from the shape: the grid (tiles x
         // K segments of the split-K kinds) bounds every segment and tile index it touches.
         const PrefillTile& t = kPrefillTable[p.kernel];
