@@ -429,3 +429,50 @@ def test_launch_rejects_prefill_plan_not_matching_its_shape(lib):
         q = Plan.from_buffer_copy(p)
         setattr(q, field, getattr(q, field) + delta)
         assert _launch(lib, q) == 1, field
+
+
+def _check(lib, p):
+    lib.w4a16_debug_check_plan.argtypes = [ctypes.POINTER(Plan)]
+    lib.w4a16_debug_check_plan.restype = ctypes.c_int
+    return lib.w4a16_debug_check_plan(ctypes.byref(p))
+
+
+def test_every_planned_shape_passes_the_launch_check(lib, monkeypatch):
+    """The launch-side check (w4a16_debug_check_plan runs it without launching) accepts every
+    plan the planner makes: auto plans over decode and prefill shapes, every forced decode shape
+    and split count the planner takes, every forced prefill config."""
+    n = 0
+    for G in (64, 128):
+        for K in (512, 1024, 4096, 8192, 8320, 14336, 28672):
+            if K % G:
+                continue
+            for N in (64, 256, 4096, 6144, 14336, 28672):
+                for M in (1, 2, 4, 5, 8, 9, 16):
+                    rc, p, err = plan(lib, M=M, N=N, K=K, G=G)
+                    assert rc == 0, err
+                    assert _check(lib, p) == 0, (M, N, K, G, p.kernel, p.decode_variant, p.splits)
+                    n += 1
+                    for v in range(32):
+                        for sp in (1, 2, 3, 4, 8):
+                            monkeypatch.setenv("W4A16_DECODE", f"{v},{sp}")
+                            rc, p, err = plan(lib, M=M, N=N, K=K, G=G)
+                            assert rc == 0, err
+                            assert _check(lib, p) == 0, (M, N, K, G, v, sp)
+                            n += 1
+                    monkeypatch.delenv("W4A16_DECODE")
+    for G in (64, 128):
+        for K in (64, 128, 4096, 4160, 8192, 8320, 14336):
+            if K % G:
+                continue
+            for N in (16, 4112, 28672):
+                for M in (1, 17, 100, 513, 2048):
+                    for cfg in [None] + list(range(1, 25)):
+                        if cfg is None:
+                            monkeypatch.delenv("W4A16_PREFILL", raising=False)
+                        else:
+                            monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+                        rc, p, err = plan(lib, M=M, N=N, K=K, G=G, variant=-1 if M > 16 or N % 64 or K % 512 else 1)
+                        assert rc == 0, err
+                        assert _check(lib, p) == 0, (M, N, K, G, cfg, p.kernel)
+                        n += 1
+    assert n > 10000

@@ -1396,18 +1396,15 @@ extern "C" int w4a16_launch_noalloc(const w4a16_plan* plan, const int32_t* Wp, c
                         base ? reinterpret_cast<int32_t*>(base) : nullptr, stream);
 }
 
-extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
-                            const uint16_t* scales, uint16_t* y, void* workspace, int32_t* counters,
-                            void* stream) {
-    if (!plan) return W4A16_ERR_INVALID;
-    const w4a16_plan& p = *plan;
-    if (p.grid <= 0 || p.M <= 0 || p.N <= 0 || p.K <= 0) return W4A16_OK;   // empty output
-    if (p.workspace_bytes && !workspace) return W4A16_ERR_WORKSPACE;
-    if (p.counter_slots && !counters) return W4A16_ERR_WORKSPACE;
+namespace {
+// Whether a plan matches what its kernel derives from (M, N, K, G): W4A16_OK, W4A16_ERR_INVALID,
+// or W4A16_ERR_WORKSPACE when a split plan declares buffers too small for its partials and
+// counters.  Pure host code.
+int check_plan(const w4a16_plan& p) {
     if ((p.G != 64 && p.G != 128) || p.K % 64 != 0 || p.N % 16 != 0 || p.K % p.G != 0) return W4A16_ERR_INVALID;
     if (p.kernel == W4A16_VARIANT_DECODE) {
-        // A decode plan must match what its shape id derives from (M, N, K): the grid, the
-        // chunks per wave and the block size bound every weight, x and y index its kernel forms.
+        // The grid, the chunks per wave and the block size bound every weight, x and y index
+        // the decode kernels form.
         if (p.decode_variant < 0 || p.decode_variant >= kNumDecodeCfg) return W4A16_ERR_INVALID;
         const DecodeCfg& c = kDecodeTable[p.decode_variant];
         const int KC = p.K >> 6;
@@ -1420,19 +1417,38 @@ extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uin
         if (p.splits > 1 && (p.counter_slots < ntiles ||
                              p.workspace_bytes < (uint64_t)p.splits * p.M * p.N * sizeof(float)))
             return W4A16_ERR_WORKSPACE;
-    } else if (p.kernel >= 1 && p.kernel <= kNumPrefillTable) {
-        // A prefill plan must match what its kernel derives from the shape: the grid (tiles x
-        // K segments of the split-K kinds) bounds every segment and tile index it touches.
-        const PrefillTile& t = kPrefillTable[p.kernel];
-        const int segs = t.kind >= 2 ? prefill_segments(p.K >> 6) : 1;
-        const int64_t tiles = ((int64_t)(p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
-        if (!prefill_shape_ok(p.kernel, p.M, p.K) || (p.splits > 1 ? p.splits : 1) != segs ||
-            (int64_t)p.grid != tiles * segs)
-            return W4A16_ERR_INVALID;
-        if (segs > 1 && ((int64_t)p.counter_slots < tiles ||
-                         p.workspace_bytes < (uint64_t)segs * p.M * p.N * sizeof(float)))
-            return W4A16_ERR_WORKSPACE;
+        return W4A16_OK;
     }
+    if (p.kernel < 1 || p.kernel > kNumPrefillTable) return W4A16_ERR_INVALID;
+    // The grid (tiles x K segments of the split-K kinds) bounds every segment and tile index a
+    // prefill kernel touches.
+    const PrefillTile& t = kPrefillTable[p.kernel];
+    const int segs = t.kind >= 2 ? prefill_segments(p.K >> 6) : 1;
+    const int64_t tiles = ((int64_t)(p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
+    if (!prefill_shape_ok(p.kernel, p.M, p.K) || (p.splits > 1 ? p.splits : 1) != segs ||
+        (int64_t)p.grid != tiles * segs)
+        return W4A16_ERR_INVALID;
+    if (segs > 1 && ((int64_t)p.counter_slots < tiles ||
+                     p.workspace_bytes < (uint64_t)segs * p.M * p.N * sizeof(float)))
+        return W4A16_ERR_WORKSPACE;
+    return W4A16_OK;
+}
+}  // namespace
+
+// Test hook (no counterpart in the reference): the launch-side plan check alone, without a launch.
+extern "C" int w4a16_debug_check_plan(const w4a16_plan* plan) {
+    return plan ? check_plan(*plan) : W4A16_ERR_INVALID;
+}
+
+extern "C" int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
+                            const uint16_t* scales, uint16_t* y, void* workspace, int32_t* counters,
+                            void* stream) {
+    if (!plan) return W4A16_ERR_INVALID;
+    const w4a16_plan& p = *plan;
+    if (p.grid <= 0 || p.M <= 0 || p.N <= 0 || p.K <= 0) return W4A16_OK;   // empty output
+    if (p.workspace_bytes && !workspace) return W4A16_ERR_WORKSPACE;
+    if (p.counter_slots && !counters) return W4A16_ERR_WORKSPACE;
+    if (const int rc = check_plan(p); rc != W4A16_OK) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const u4* wp = reinterpret_cast<const u4*>(Wp);
     hipError_t e = hipSuccess;
