@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X W4A16 GEMM on BASELINE.json's metric.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill|quantize]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload decode|prefill|moderate|c1|quantize|gemv|copy]
                     [--no-cpu] [--no-prefill] [--json PATH]
 
 Headline (default): decode GB/s on the Llama-3-8B MLP shapes,
@@ -489,9 +490,10 @@ def main(argv=None) -> int:
     ap.add_argument("--prefill-warmup", type=int, default=60,
                     help="untimed prefill calls before the prefill leg of the decode run: the clock settles "
                          "after ~50 calls of this power-bound shape")
-    ap.add_argument("--workload", choices=("decode", "prefill", "moderate", "quantize", "gemv", "copy"),
+    ap.add_argument("--workload", choices=("decode", "prefill", "moderate", "c1", "quantize", "gemv", "copy"),
                     default="decode",
-                    help="prefill: configs[3] alone; moderate: configs[2] alone; quantize: device quantise+pack of "
+                    help="prefill: configs[3] alone; moderate: configs[2] alone; c1: configs[0] alone (w4a16_gemm, "
+                         "M=1, K=N=4096); quantize: device quantise+pack of "
                          "the prefill weight; gemv: the baseline GEMV (w4a16_ext); copy: HBM-counter calibration "
                          "kernel (64 MiB elementwise copy), no benchmark line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -575,6 +577,30 @@ def main(argv=None) -> int:
                             "unit": "TFLOP/s", "frac": round(mod["TFLOPs"] / FP16_MFMA_PEAK_TFS, 4),
                             "frac_hbm": round(mod["GBs"] / HBM_PEAK_GBS, 4), "kernel": mod["kernel"],
                             "flops_per_launch": alg_flops(M, N, K), "bytes_per_launch": alg_bytes(M, N, K, Gm)}}
+        tag_counters(out["roofline"], "moderate", [mod["kernel"]], ["traffic", "mfma_busy_frac", "clock_ghz"])
+        line = json.dumps(out)
+        print(line, flush=True)
+        if a.json:
+            with open(a.json, "w") as f:
+                f.write(line + "\n")
+        return 0
+    if a.workload == "c1":
+        c1 = bench_c1(torch, gemm, a.steps, a.warmup)
+        name, N, K, M = C1_CASE
+        out = {"metric": "decode GB/s & %HBM peak at BASELINE configs[0] (w4a16_gemm, M=1, K=N=4096, G=128)",
+               "value": round(c1["GBs"], 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+               "ms_per_step": round(c1["us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+               "vs_baseline": None, "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
+               "config": {"workload": "BASELINE configs[0]: w4a16_gemm decode M=1 K=4096 N=4096 G=128; one step = "
+                                      "one call", "weight_copies": c1["copies"],
+                          "reference_published": "58.94 us median on an RTX 3050 Laptop GPU "
+                                                 "(benchmarks/results/latest.json:368-384)"},
+               "roofline": {"bound": "hbm", "achieved": round(c1["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(c1["GBs"] / HBM_PEAK_GBS, 4), "kernel": c1["kernel"],
+                            "bytes_per_launch": alg_bytes(M, N, K), "avg_launch_us": round(c1["us"], 3)}}
+        tag_counters(out["roofline"], "c1", [c1["kernel"]], ["traffic"])
+        if not a.no_cpu:
+            out["cpu_baseline"] = cpu_baseline([C1_CASE])
         line = json.dumps(out)
         print(line, flush=True)
         if a.json:
@@ -649,6 +675,7 @@ def main(argv=None) -> int:
             "roofline": {"bound": "hbm", "achieved": round(c1["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(c1["GBs"] / HBM_PEAK_GBS, 4), "kernel": c1["kernel"],
                          "bytes_per_launch": alg_bytes(M, N, K)}}
+        tag_counters(out["decode_c1"]["roofline"], "c1", [c1["kernel"]], ["traffic"])
     if gv is not None:
         out["baseline_gemv"] = {"value": round(gv["value"], 1), "unit": "GB/s",
                                 "frac_hbm": round(gv["value"] / HBM_PEAK_GBS, 4),
