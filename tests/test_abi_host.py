@@ -184,6 +184,8 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (17, 4096, 14336, 17), (32, 6144, 4096, 17), (32, 14336, 4096, 17),     # token groups of 16
     (33, 4096, 4096, 17), (64, 4096, 4096, 17), (48, 14336, 4096, 10), (128, 6144, 4096, 10),
     (32, 28672, 4096, 10),                                                   # token groups of 32
+    (256, 4096, 4096, 10), (128, 8192, 4096, 10), (64, 16384, 4096, 10),     # exactly 4 two-block waves per CU
+    (256, 4160, 4096, 14),                                                   # just above: two blocks per wave
     # long K (4 or 7 segments): split-K token groups, larger groups sooner
     (64, 4096, 14336, 10), (128, 4096, 14336, 12), (256, 4096, 14336, 13), (512, 4096, 14336, 18),
     (17, 8192, 28672, 12), (192, 8192, 28672, 13), (384, 8192, 28672, 19),
