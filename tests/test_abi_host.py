@@ -189,6 +189,7 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     # long K (4 or 7 segments): split-K token groups, larger groups sooner
     (64, 4096, 14336, 10), (128, 4096, 14336, 12), (256, 4096, 14336, 13), (512, 4096, 14336, 18),
     (17, 8192, 28672, 12), (192, 8192, 28672, 13), (384, 8192, 28672, 19),
+    (64, 8192, 28672, 13), (96, 8192, 28672, 12), (100, 14336, 14336, 13),  # 64-token groups when they pad no more
     (2048, 4096, 14336, 24), (1024, 8192, 28672, 24), (2048, 8192, 28672, 24),  # long K, 128 x 256: last round > half full
     (768, 8192, 28672, 24), (1536, 4096, 14336, 24), (512, 8192, 28672, 19), (1024, 4096, 14336, 20),
     (3072, 4096, 14336, 7), (1536, 8192, 28672, 7),                         # long K, >= 2 rounds of 128 x 128: two 128 x 64 waves

@@ -144,7 +144,11 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         if (M >= 384 && wide_tiles(19) >= 0.75 * cus) return 19;
         if (M >= 256 && wide_tiles(18) >= 0.75 * cus) return 18;
         if (group_ok(17) && group_waves(17) <= 9.0 * cus) return 17;
-        if (M >= 128 && group_ok(13) && group_waves(12) >= 13.0 * cus) return 13;
+        // 64-token groups once config 12's waves exceed 13 per CU, from M = 64 when they pad no more
+        // rows than 32-token groups (M = 64: 61.9-62.2 vs 69.2-70.4 us at N = K = 14336, 68.5-69.0 vs
+        // 70.4-71.3 at N = 8192, K = 28672; M = 96, a half-empty second group: 105 vs 95.5).
+        const bool pad64_ok = M >= 128 || (M >= 64 && (M + 63) / 64 * 64 == (M + 31) / 32 * 32);
+        if (pad64_ok && group_ok(13) && group_waves(12) >= 13.0 * cus) return 13;
         if (group_ok(12) && group_waves(12) >= 5.0 * cus) return 12;
         if (group_ok(10) && group_waves(10) <= 8.0 * cus) return 10;
         if (wide_tiles(20) >= 0.75 * cus) return 20;

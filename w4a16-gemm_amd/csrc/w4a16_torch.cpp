@@ -58,8 +58,14 @@ bool capturing(hipStream_t stream) {
 void ensure_capture_pool(const at::Tensor& like) {
     const int dev = (int)like.device().index();
     std::lock_guard<std::mutex> lk(g_mu);
-    if (!g_capture_pool.count(dev))
-        g_capture_pool[dev].buf = torch::zeros({kCapturePoolSlots}, like.options().dtype(torch::kInt32));
+    if (!g_capture_pool.count(dev)) {
+        at::Tensor buf = torch::zeros({kCapturePoolSlots}, like.options().dtype(torch::kInt32));
+        // The zero fill runs on the current stream, and captured launches may later run on another
+        // one: wait for it here, once per device (never under capture: the caller checks).
+        TORCH_CHECK(hipStreamSynchronize(c10::hip::getCurrentHIPStream(dev).stream()) == hipSuccess,
+                    "w4a16_gemm: hipStreamSynchronize failed");
+        g_capture_pool[dev].buf = buf;
+    }
 }
 
 at::Tensor split_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
