@@ -161,8 +161,11 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         if (rounds24 > 0.5 && rounds24 <= 1.0) return 24;
     }
     if (wide_tiles(5) >= 0.75 * cus) return 5;
-    if (M >= 128 && wide_tiles(20) >= 0.75 * cus) return 20;
-    if (M >= 64 && wide_tiles(22) >= 0.75 * cus) return 22;
+    // The 128 x 128 and pipelined 64 x 128 tiles from 0.6 of the CUs: at 62.5% (Llama-3-70B qkv,
+    // N = 10240, K = 8192) they beat the token groups (M = 128: 43.4 vs 57.5 us; M = 256: 64.9 vs
+    // 69.5 for the 64 x 128 tiles); at 50% (70B o, N = 8192, M = 128) they lose (43.3 vs 38.0).
+    if (M >= 128 && wide_tiles(20) >= 0.6 * cus) return 20;
+    if (M >= 64 && wide_tiles(22) >= 0.6 * cus) return 22;
     const double blocks = std::ceil(N / 16.0);
     if (prefill_occupancy(17, lim) > 0 && prefill_shape_ok(17, M, K) &&
         std::ceil(M / 16.0) * blocks <= 8.0 * cus)
@@ -291,8 +294,9 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             // the first that fits wins:
             //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): refill-ahead
             //    rings of 4 waves, 2 blocks while the x rows are few (M <= 8: M = 8, 9.51 vs
-            //    9.88 us), else 4 blocks (M = 16: 10.05 vs 11.16 us); no split.  Twice as wide (fused gate/up, N = 28672): single-block rings of 8 waves
-            //    at M = 1 (14.6 vs 16.8 us), of 4 waves with 4 pairs in flight at M <= 4;
+            //    9.88 us), else 4 blocks (M = 16: 10.05 vs 11.16 us); no split.  Twice as wide (fused gate/up, N = 28672): single-block rings
+            //    of 4 waves with 4 pairs in flight at M <= 4 (M = 1 in four sweeps at K = 4096 and 8192:
+            //    14.27-15.05 vs 15.15-15.33 us and 25.69-25.86 vs 25.83-27.58 for 8 waves with 3 pairs);
             //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves,
             //    3 pairs in flight up to 4 token rows and 2 up to 8 rows; above 8 rows, where the x
             //    traffic per block grows, two-block tiles of 4 waves split in two (M = 16: 11.95
@@ -317,7 +321,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
                 return (int64_t)ntiles_of(cand) * sp <= (int64_t)per_cu * cus;
             };
             struct Cand { int v, sp; };
-            Cand vwide_m1[] = {{29, 1}, {20, 1}, {12, 1}};
+            Cand vwide_m1[] = {{21, 1}, {29, 1}, {20, 1}};
             Cand vwide_small_m[] = {{21, 1}, {20, 1}, {12, 1}};
             Cand wide_small_m[] = {{20, 1}, {12, 1}, {7, 1}};
             Cand wide[] = {{16, 1}, {12, 1}, {7, 1}};
@@ -330,6 +334,17 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             Cand many_longk_m4[] = {{30, 1}, {26, 1}, {29, 1}};
             Cand many_small_m[] = {{26, 1}, {22, 1}, {19, 1}};
             Cand many_longk_large_m[] = {{16, 2}, {26, 1}, {20, 2}};
+            // K = 8192 with many blocks (Llama-3-70B o, qkv): shorter streams than the 70B down
+            // projection the lists above come from, so no split; two-block tiles while they fit one
+            // per CU (o, N = 8192: M = 4 9.28 vs 9.93 us, M = 16 10.84 vs 13.15), else single-block
+            // rings below 8 rows and four-block tiles above (qkv, N = 10240: M = 1 12.07 vs 14.03,
+            // M = 4 12.87 vs 16.38, M = 8 14.34 vs 16.66, M = 16 15.60 vs 28.25).
+            Cand k8k_fit_small_m[] = {{26, 1}, {29, 1}, {19, 1}};
+            Cand k8k_fit_large_m[] = {{20, 1}, {28, 1}, {26, 1}};
+            Cand k8k_m1[] = {{29, 1}, {25, 1}, {19, 1}};
+            Cand k8k_m4[] = {{19, 1}, {29, 1}, {22, 1}};
+            Cand k8k_m8[] = {{31, 1}, {19, 1}, {18, 1}};
+            Cand k8k_large_m[] = {{16, 1}, {18, 1}, {17, 1}};
             Cand* list;
             const int n = 3;
             const bool very_wide = (int64_t)ntiles_of(12) * 2 >= 3LL * cus;
@@ -338,6 +353,10 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
                 list = M <= 1 ? vwide_m1 : M <= 4 ? vwide_small_m : wide;
             else if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus)
                 list = M <= 8 ? wide_small_m : wide;
+            else if (KC == 128 && many_blocks && ntiles_of(26) <= cus)
+                list = M <= 8 ? k8k_fit_small_m : k8k_fit_large_m;
+            else if (KC == 128 && many_blocks)
+                list = M <= 1 ? k8k_m1 : M <= 4 ? k8k_m4 : M <= 8 ? k8k_m8 : k8k_large_m;
             else if (KC >= 128 && many_blocks)
                 list = M <= 1 ? many_m1 : M <= 4 ? many_longk_m4 : M <= 8 ? many_small_m : many_longk_large_m;
             else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
