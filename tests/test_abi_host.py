@@ -341,7 +341,9 @@ def test_gcn_arch_name_parse(lib, name, want):
     (16, 4096, 4096, (19, 1)), (16, 6144, 4096, (20, 1)),                    # qkv: 384 single-block rings = 2 rounds
     (1, 6144, 4096, (29, 1)), (4, 6144, 4096, (26, 1)), (8, 6144, 4096, (26, 1)),  # qkv: two-block rings below 16 rows
     (1, 8192, 28672, (26, 1)), (4, 8192, 28672, (30, 1)), (8, 8192, 28672, (26, 1)),  # 70B down: 512 single blocks
-    (16, 8192, 28672, (16, 2))])
+    (16, 8192, 28672, (16, 2)),
+    (1, 3584, 18944, (21, 1)), (16, 3584, 18944, (21, 1)),                  # odd chunks per 8-wave ring: generic rings
+    (1, 5120, 13824, (21, 1)), (8, 5120, 13824, (20, 1)), (16, 18944, 3584, (20, 1))])
 def test_decode_selection(lib, M, N, K, want):
     """The decode shapes the planner picks for the Llama-3 projections (BASELINE configs[1] first)."""
     rc, p, err = plan(lib, M=M, N=N, K=K, G=128)

@@ -141,7 +141,9 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
         }
         if (M >= 1024 && wide_tiles(7) >= 2.0 * cus) return 7;
         if (M >= 1024 && wide_tiles(20) >= 0.75 * cus) return 20;
-        if (M >= 384 && wide_tiles(19) >= 0.75 * cus) return 19;
+        // From 0.6 of the CUs, as the K <= 8192 wide tiles (Llama-2-13B down, N = 5120, K = 13824,
+        // M = 512, 160 tiles of 64 x 256: 109.8 vs 136.8 us for the 64-token groups).
+        if (M >= 384 && wide_tiles(19) >= 0.6 * cus) return 19;
         if (M >= 256 && wide_tiles(18) >= 0.75 * cus) return 18;
         if (group_ok(17) && group_waves(17) <= 9.0 * cus) return 17;
         // 64-token groups once config 12's waves exceed 13 per CU, from M = 64 when they pad no more
@@ -366,6 +368,22 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
                     (M <= 8 || one_round(list[i].v, list[i].sp))) {
                     var = list[i].v; splits = list[i].sp;
                 }
+            // Shapes the lists above do not fit (a K whose chunks per wave are odd for 8-wave rings,
+            // e.g. 13824 and 18944, or rings that would need two rounds above 8 rows): the ring
+            // kernels still beat the fallbacks below by 1.7-3.5x.  Single-block 4-wave rings with 4
+            // pairs in flight up to 4 rows, and above while single-block tiles fit one per CU;
+            // two-block rings otherwise (Qwen2-7B down, N = 3584, K = 18944, M = 1..16: 11.2-15.9 us
+            // against 39-49 for the fallback; Llama-2-13B down, N = 5120, K = 13824, M = 1..16:
+            // 12.3-16.2 against 22.6-27.8; Qwen2-7B gate, N = 18944, K = 3584, M = 16: 13.6 vs 23.8).
+            if (var < 0) {
+                Cand gen_fit[] = {{21, 1}, {28, 1}, {20, 1}};
+                Cand gen_many[] = {{20, 1}, {28, 1}, {21, 1}};
+                Cand* gen = (M <= 4 || N / 16 <= cus) ? gen_fit : gen_many;
+                for (int i = 0; i < 3 && var < 0; ++i)
+                    if (ok(gen[i].v, gen[i].sp) && (int64_t)ntiles_of(gen[i].v) * gen[i].sp * 2 >= cus) {
+                        var = gen[i].v; splits = gen[i].sp;
+                    }
+            }
             if (var < 0 && KC >= 128) {
                 for (int sp = 1; sp <= KC; ++sp)
                     if (ok(6, sp) && ((int64_t)ntiles_of(6) * sp >= cus || KC / (sp * 8) <= 4)) {
