@@ -193,6 +193,7 @@ PREFILL_TILES = {1: (16, 128), 2: (32, 128), 3: (64, 128), 4: (128, 128), 5: (12
     (2048, 4096, 14336, 24), (1024, 8192, 28672, 24), (2048, 8192, 28672, 24),  # long K, 128 x 256: last round > half full
     (768, 8192, 28672, 24), (1536, 4096, 14336, 24), (512, 8192, 28672, 19), (1024, 4096, 14336, 20),
     (3072, 4096, 14336, 7), (1536, 8192, 28672, 7),                         # long K, >= 2 rounds of 128 x 128: two 128 x 64 waves
+    (2048, 5120, 13824, 20),                                                 # 2.5 rounds: last round half empty
     (40, 4096, 4160, None)])                                                 # odd chunk count: classic
 def test_prefill_wide_selection(lib, M, N, K, want):
     rc, p, err = plan(lib, M=M, N=N, K=K, G=64)

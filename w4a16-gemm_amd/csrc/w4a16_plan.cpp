@@ -139,7 +139,13 @@ int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
             const double rounds = wide_tiles(24) / cus;
             if (rounds > 0.5 && std::ceil(rounds) - rounds < 0.5) return 24;
         }
-        if (M >= 1024 && wide_tiles(7) >= 2.0 * cus) return 7;
+        // Config 7 once its tiles fill two rounds of the CUs and its last round is more than half full,
+        // as for the 128 x 512 and 128 x 256 tiles (Llama-2-13B down, N = 5120, K = 13824, M = 2048:
+        // 2.5 rounds, 394 us against 343 for config 20).
+        if (M >= 1024) {
+            const double rounds7 = wide_tiles(7) / cus;
+            if (rounds7 >= 2.0 && std::ceil(rounds7) - rounds7 < 0.5) return 7;
+        }
         if (M >= 1024 && wide_tiles(20) >= 0.75 * cus) return 20;
         // From 0.6 of the CUs, as the K <= 8192 wide tiles (Llama-2-13B down, N = 5120, K = 13824,
         // M = 512, 160 tiles of 64 x 256: 109.8 vs 136.8 us for the 64-token groups).
