@@ -34,7 +34,11 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 1
+/* ABI version.  2: prefill plans may split K over workgroups (splits > 1, counter_slots and
+ * workspace_bytes set, kernel ids 1..24), and the decode shape ids behind W4A16_DECODE were
+ * renumbered; a caller written for version 1 (scratch only for decode split-K) must size the
+ * workspace and counters from every plan. */
+#define W4A16_ABI_VERSION 2
 
 /* Status codes. */
 #define W4A16_OK            0
@@ -118,11 +122,16 @@ int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
  * harnesses that forbid hipMalloc.  It allocates nothing (no hipMalloc, no allocating library
  * call); the caller passes only the inputs and y.  Runs on the current HIP device, on `stream`.
  * The first call on a device resolves the array's address and clears its counters with a small
- * kernel on `stream`.  Every call on one GPU shares that GPU's array: calls whose plans have
- * workspace_bytes > 0 must not overlap in time on one GPU (they race on the partials and
- * counters); plans without a workspace (prefill, unsplit decode) use no scratch.
- * Returns W4A16_OK, W4A16_ERR_WORKSPACE when plan->workspace_bytes exceeds
- * W4A16_NOALLOC_MAX_WORKSPACE_BYTES or plan->counter_slots exceeds W4A16_NOALLOC_MAX_COUNTER_SLOTS
+ * kernel on `stream`; make that first call outside graph capture (under capture the clear would be
+ * recorded into the graph instead of running now).  Later calls may be captured: the graph
+ * replays them against the same array.  Every call on one GPU shares that GPU's array: calls whose
+ * plans have workspace_bytes > 0 must not overlap in time on one GPU (they race on the partials and
+ * counters); plans without a workspace (unsplit prefill and decode) use no scratch.
+ * A prefill plan whose partials or counters exceed the array (long K at moderate M, which splits K
+ * over workgroups) runs as a scratch-free config of the same problem instead: every prefill
+ * config gives the same bits.
+ * Returns W4A16_OK, W4A16_ERR_WORKSPACE when a decode plan's workspace_bytes exceeds
+ * W4A16_NOALLOC_MAX_WORKSPACE_BYTES or its counter_slots exceed W4A16_NOALLOC_MAX_COUNTER_SLOTS
  * (message via w4a16_last_error), or W4A16_ERR_HIP. */
 int w4a16_launch_noalloc(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
                          const uint16_t* scales, uint16_t* y, void* stream);

@@ -9,7 +9,8 @@ import pytest
 
 from oracle import quant
 
-PKG = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "w4a16-gemm_amd")
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "w4a16-gemm_amd")
 
 
 def torch_cuda():

@@ -69,7 +69,7 @@ def test_library_exports_every_declared_symbol(lib):
     assert len(names) >= 6, names
     for n in names:
         assert hasattr(lib, n), f"libw4a16_hip.so does not export {n}"
-    assert lib.w4a16_abi_version() == 1
+    assert lib.w4a16_abi_version() == 2
 
 
 def test_plan_struct_layout_matches_header(lib):
@@ -484,3 +484,45 @@ def test_every_planned_shape_passes_the_launch_check(lib, monkeypatch):
                         assert _check(lib, p) == 0, (M, N, K, G, cfg, p.kernel)
                         n += 1
     assert n > 10000
+
+
+# Wide-tile configs (kind 1) address x and the weights with 32-bit per-lane byte offsets from a
+# 64-bit base: (bm - 1) * K * 2 + 112 bytes into the tile's x rows and K * 8 + 496 bytes into the
+# second n16 block of a pair.  The planner must never hand them a K for which these wrap (the
+# contract allows any K that fits int32, kernel.cu:228).
+WIDE_BM = {5: 128, 6: 256, 7: 128, 18: 64, 19: 64, 20: 128, 21: 256, 22: 64, 23: 128, 24: 128}
+
+
+def _wide_offsets_fit(bm, K):
+    return (bm - 1) * K * 2 + 128 <= 2**32 and K * 8 + 512 <= 2**31 - 1
+
+
+@pytest.mark.parametrize("cfg", sorted(WIDE_BM))
+def test_wide_configs_refused_where_32bit_offsets_wrap(lib, monkeypatch, cfg):
+    bm = WIDE_BM[cfg]
+    kmax = (2**32 - 128) // (2 * (bm - 1)) // 128 * 128          # largest K (multiple of 128) that fits
+    monkeypatch.setenv("W4A16_PREFILL", str(cfg))
+    for K in (kmax - 128 * 64, kmax, kmax + 128, kmax + 128 * 64, 2**23 + 2**16, 2**24 + 2**16):
+        rc, p, err = plan(lib, M=2 * bm + 1, N=4096, K=K, G=128)
+        assert rc == 0, err
+        if p.kernel == cfg:
+            assert _wide_offsets_fit(bm, K), (cfg, K)
+        if not _wide_offsets_fit(bm, K):
+            assert p.kernel != cfg and _check(lib, p) == 0, (cfg, K, p.kernel)
+        chosen_bm = WIDE_BM.get(p.kernel)
+        assert chosen_bm is None or _wide_offsets_fit(chosen_bm, K), (cfg, K, p.kernel)
+
+
+def test_auto_plan_at_k_beyond_the_256_row_wide_tiles(lib):
+    """K = 2^23 + 2^16: the 256-row wide tiles (configs 6, 21) would wrap their x offsets; the auto
+    plan takes a config whose addresses fit, and passes the launch-side check."""
+    K = 2**23 + 2**16
+    assert not _wide_offsets_fit(256, K) and _wide_offsets_fit(128, K)
+    for M in (17, 300, 2048):
+        rc, p, err = plan(lib, M=M, N=4096, K=K, G=128)
+        assert rc == 0, err
+        assert _check(lib, p) == 0
+        assert WIDE_BM.get(p.kernel, 0) != 256
+    rc, p, err = plan(lib, M=2048, N=4096, K=2**24 + 128, G=128)
+    assert rc == 0 and _check(lib, p) == 0
+    assert p.kernel not in WIDE_BM or _wide_offsets_fit(WIDE_BM[p.kernel], 2**24 + 128)

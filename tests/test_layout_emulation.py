@@ -568,3 +568,26 @@ def test_group_split_k_covers_every_tile_segment_and_pair(groups_m, cols, KC, D)
         assert npair >= D
         covered += list(range(pair0, pair0 + npair))
     assert covered == list(range(KC // 2))
+
+
+@pytest.mark.parametrize("cfg", sorted(WIDE_TILES))
+def test_wide_prefill_offsets_at_the_largest_planned_k(cfg):
+    """The per-lane 32-bit byte offsets of prefill_wide_kernel (weights: second block of a pair,
+    x: rows below the tile's first row) computed without wrapping at the largest K the planner
+    gives the config (prefill_wide_offsets_fit): every one is below 2^32 (weights below 2^31, as
+    it is formed in int).  One 128-step larger K would wrap the x offset, so the bound is tight."""
+    BM, BN, WMs, WNs = WIDE_TILES[cfg]
+    NT = WMs * WNs * 64
+    kmax = (2**32 - 128) // (2 * (BM - 1)) // 128 * 128
+    for K in (kmax, kmax + 128):
+        KC = K // 64
+        M = BM + 5                                     # two M tiles: the first has BM rows below m0
+        wmax = max(nbl * KC * 512 + (((r & 7) << 2) | (tp << 1) | kg) * 16
+                   for nbl in (0, 1) for r in range(32) for tp in (0, 1) for kg in (0, 1))
+        xmax = max(((min(0 + (sg >> 3), M - 1) - 0) * K + (sg & 7) * 8) * 2 + 16
+                   for tid in range(NT) for i in range(BM * 8 // NT) for sg in [tid + i * NT])
+        assert wmax < 2**31
+        if K == kmax:
+            assert xmax <= 2**32, (cfg, K, xmax)
+        else:
+            assert xmax > 2**32, (cfg, K, xmax)

@@ -417,6 +417,32 @@ def test_cuda_graph_capture_split_k(M):
     assert_close(y, ref_gemm(x, q, scales, G, key))
 
 
+@pytest.mark.parametrize("M", [12, 33])
+def test_graph_capture_without_warm_up_call(M):
+    """Capture with no capture pool on the device (as in a process whose first call is captured):
+    the captured split-K call zeroes counters of its own with a fill kernel recorded in the graph.
+    Three replays, with eager split-K calls (which recreate the pool) between them, each equal to
+    the eager result."""
+    torch = torch_cuda()
+    import w4a16_opt
+    N, K, G = 256, 14336, 128
+    assert w4a16_opt.plan_info(M, N, K, G)["splits"] > 1
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=47)
+    torch.cuda.synchronize()
+    w4a16_opt._debug_drop_capture_pool(torch.cuda.current_device())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = gemm(Wp, x, scales)
+    for rep in range(3):
+        x.copy_(torch.randn(x.shape, device="cuda").half())
+        g.replay()
+        torch.cuda.synchronize()
+        eager = gemm(Wp, x, scales)
+        torch.cuda.synchronize()
+        assert torch.equal(eager, y), f"replay {rep} differs from the eager result"
+    assert_close(y, ref_gemm(x, q, scales, G, key))
+
+
 @pytest.mark.parametrize("G", [64])
 def test_baseline_c5_ragged_rows_independent(G):
     """Config 5: N=4112 (N%64 != 0), K=4160, 65 groups, outliers; rows independent of M."""

@@ -130,3 +130,79 @@ def test_noalloc_rejects_plans_beyond_the_scratch(monkeypatch):
     rc = L.w4a16_launch_noalloc(ctypes.byref(plan), 0, 0, 0, 0, torch.cuda.current_stream().cuda_stream)
     assert rc == W4A16_ERR_WORKSPACE
     assert b"static scratch" in L.w4a16_last_error()
+
+
+def test_noalloc_long_k_moderate_m_runs_scratch_free():
+    """Long K at moderate M: the auto plan splits K over workgroups and its partials (8 and 16 MiB)
+    exceed the static scratch; the entry point runs a scratch-free config of the same problem
+    instead, bit for bit equal to w4a16_launch with a workspace, allocating nothing."""
+    torch = torch_cuda()
+    L = _lib()
+    G = 128
+    x, q, scales, Wp, key = make_problem(256, 4096, 14336, G, seed=54)
+    for m in (128, 256):
+        print(f"noalloc long-K prefill beyond the scratch: M={m} N=4096 K=14336", flush=True)
+        xm = x[:m].contiguous()
+        plan = _plan(L, torch, Wp, xm, scales, G)
+        assert plan.kernel >= 1 and plan.splits > 1 and plan.workspace_bytes > 4 << 20, (plan.kernel, plan.splits)
+        y_na = torch.empty(m, 4096, dtype=torch.half, device="cuda")
+        st = torch.cuda.current_stream().cuda_stream
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        rc = L.w4a16_launch_noalloc(ctypes.byref(plan), Wp.data_ptr(), xm.data_ptr(), scales.data_ptr(),
+                                    y_na.data_ptr(), st)
+        torch.cuda.synchronize()
+        assert rc == 0, L.w4a16_last_error()
+        assert torch.cuda.mem_get_info()[0] == free0
+        y_na2, y, _ = _both(L, torch, Wp, xm, scales, G)
+        assert torch.equal(y_na, y) and torch.equal(y_na2, y)
+        assert torch.equal(y, gemm(Wp, xm, scales))
+        assert_close(y_na, ref_gemm(xm, q, scales, G, key))
+
+
+def test_noalloc_replayed_under_graph_capture():
+    """After one eager call on the device, noalloc launches captured into a HIP graph (a split-K
+    decode plan whose counters and partials sit in the static scratch, and a long-K prefill plan)
+    replay correctly: three replays with eager work between them, each bit for bit equal to the
+    eager result; an eager call allocates no device memory."""
+    torch = torch_cuda()
+    L = _lib()
+    G = 128
+    xd, qd, sd, Wd, keyd = make_problem(16, 256, 14336, G, seed=55)
+    xp, qp, sp, Wpp, keyp = make_problem(40, 1024, 14336, G, seed=56)
+    pd = _plan(L, torch, Wd, xd, sd, G)
+    pp = _plan(L, torch, Wpp, xp, sp, G)
+    assert pd.kernel == 0 and pd.splits > 1 and pp.kernel >= 1 and pp.splits > 1
+    st = torch.cuda.current_stream().cuda_stream
+    yd_e = torch.empty(16, 256, dtype=torch.half, device="cuda")
+    yp_e = torch.empty(40, 1024, dtype=torch.half, device="cuda")
+    print("noalloc eager calls before capture", flush=True)
+    assert L.w4a16_launch_noalloc(ctypes.byref(pd), Wd.data_ptr(), xd.data_ptr(), sd.data_ptr(), yd_e.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    assert L.w4a16_launch_noalloc(ctypes.byref(pp), Wpp.data_ptr(), xp.data_ptr(), sp.data_ptr(), yp_e.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    yd_g = torch.empty_like(yd_e)
+    yp_g = torch.empty_like(yp_e)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    print("noalloc capture", flush=True)
+    with torch.cuda.graph(g, stream=s):
+        cs = torch.cuda.current_stream().cuda_stream
+        assert L.w4a16_launch_noalloc(ctypes.byref(pd), Wd.data_ptr(), xd.data_ptr(), sd.data_ptr(), yd_g.data_ptr(), cs) == 0
+        assert L.w4a16_launch_noalloc(ctypes.byref(pp), Wpp.data_ptr(), xp.data_ptr(), sp.data_ptr(), yp_g.data_ptr(), cs) == 0
+    for r in range(3):
+        print(f"noalloc replay {r}", flush=True)
+        yd_g.zero_()
+        yp_g.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yd_g, yd_e) and torch.equal(yp_g, yp_e), r
+        # eager work between replays, through the same scratch
+        assert L.w4a16_launch_noalloc(ctypes.byref(pd), Wd.data_ptr(), xd.data_ptr(), sd.data_ptr(),
+                                      yd_e.data_ptr(), st) == 0
+        torch.cuda.synchronize()
+    assert_close(yd_e, ref_gemm(xd, qd, sd, G, keyd))
+    assert_close(yp_e, ref_gemm(xp, qp, sp, G, keyp))

@@ -3,6 +3,8 @@
 #pragma once
 #include <stdint.h>
 
+#include "w4a16.h"
+
 namespace w4a16 {
 
 // Prefill tile configurations.  Ids 1..4 are the forced variants of the reference API (its
@@ -107,6 +109,14 @@ constexpr int prefill_wide_steps(int cfg, bool seg) {
                ? 2
                : kPrefillTable[cfg].depth;
 }
+// The wide kernels (kind 1) address x and the weights with 32-bit per-lane byte offsets from a
+// wave-uniform 64-bit base: x rows up to bm - 1 below the tile's first row ((bm - 1) * K * 2 + 112
+// bytes) and the second n16 block of a 32-channel pair (K * 8 + 496 bytes, formed in int).  Longer
+// K goes to the other kinds, whose addresses are 64-bit throughout.
+constexpr bool prefill_wide_offsets_fit(int cfg, int K) {
+    return (int64_t)(kPrefillTable[cfg].bm - 1) * K * 2 + 128 <= ((int64_t)1 << 32) &&
+           (int64_t)K * 8 + 512 <= ((int64_t)1 << 31) - 1;
+}
 // Kinds 1..3 walk K two chunks at a time; kinds 2 and 3 need at least `depth` chunk pairs in
 // every segment and kind 2 covers all M in one tile; kind 1 walks K `depth` chunks at a time
 // and, with several segments, needs the registers of a second accumulator set and segments of
@@ -115,7 +125,7 @@ constexpr bool prefill_shape_ok(int cfg, int M, int K) {
     return kPrefillTable[cfg].kind == 0 ||
            ((K / 64) % 2 == 0 &&
             (kPrefillTable[cfg].kind == 1
-                 ? (prefill_segments(K / 64) == 1
+                 ? prefill_wide_offsets_fit(cfg, K) && (prefill_segments(K / 64) == 1
                         ? (K / 64) % prefill_wide_steps(cfg, false) == 0
                         : prefill_wide_segmentable(cfg) && (K / 64) % prefill_wide_steps(cfg, true) == 0 &&
                               prefill_segment_chunks(K / 64) % prefill_wide_steps(cfg, true) == 0)
@@ -172,6 +182,11 @@ constexpr bool decode_shape_fits(int v, int KC, int splits, int G) {
 
 // Counter buffer size (ints) the library may ask for: one per decode column tile.
 constexpr int32_t kMaxCounterSlots = 1 << 18;
+
+// A plan for the same prefill problem as `in` whose config needs no split-K scratch (prefill
+// configs all give the same bits); false when `in` is not a prefill plan or none fits.
+// Defined in w4a16_plan.cpp; used by w4a16_launch_noalloc.
+bool prefill_plan_no_scratch(const w4a16_plan& in, const w4a16_device_limits& lim, w4a16_plan* out);
 
 }  // namespace w4a16
 

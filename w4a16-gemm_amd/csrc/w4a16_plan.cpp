@@ -62,6 +62,26 @@ int prefill_occupancy(int cfg, const w4a16_device_limits& lim) {
 // dequantisation overhead D, paid once per weight column block and wave row (D = 32 rows for
 // prefill_kernel, 16 for the wide wave tiles whose dequantised operands feed twice as many
 // MFMAs).
+// The launch fields of a prefill plan for config `cfg` (p->M, N, K, G set): kinds 2 and 3 run one
+// canonical K segment per workgroup (split-K partials and one counter per tile), the others all
+// of K.  False when the grid does not fit int32.
+bool fill_prefill_plan(int cfg, w4a16_plan* p) {
+    const int KC = p->K / 64;
+    const int segs = prefill_segments(KC);
+    const PrefillTile& t = kPrefillTable[cfg];
+    const int64_t tiles = ((int64_t)(p->M + t.bm - 1) / t.bm) * ((p->N + t.bn - 1) / t.bn);
+    const int splits = t.kind >= 2 ? segs : 1;
+    if (tiles * splits > std::numeric_limits<int32_t>::max()) return false;
+    p->kernel = cfg;
+    p->block = prefill_threads(cfg);
+    p->grid = (int32_t)(tiles * splits);
+    p->splits = splits;
+    p->slab_chunks = prefill_segment_chunks(KC);
+    p->counter_slots = splits > 1 ? (int32_t)tiles : 0;
+    p->workspace_bytes = splits > 1 ? (uint64_t)splits * p->M * p->N * sizeof(float) : 0;
+    return true;
+}
+
 int prefill_select(int M, int N, int K, const w4a16_device_limits& lim) {
     int best = 0;
     double best_cost = std::numeric_limits<double>::infinity();
@@ -448,17 +468,8 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             return ((int64_t)(M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
         };
         if (kPrefillTable[cfg].kind >= 2 && segs > 1 && tiles_of(cfg) > kMaxCounterSlots) cfg = 4;
-        const int64_t tiles = tiles_of(cfg);
-        const int splits = kPrefillTable[cfg].kind >= 2 ? segs : 1;
-        if (tiles * splits > std::numeric_limits<int32_t>::max())
+        if (!fill_prefill_plan(cfg, &out))
             return fail(W4A16_ERR_INVALID, err, errlen, "M too large for prefill config %d", cfg);
-        out.kernel = cfg;
-        out.block = prefill_threads(cfg);
-        out.grid = (int32_t)(tiles * splits);
-        out.splits = splits;
-        out.slab_chunks = prefill_segment_chunks(KC);
-        out.counter_slots = splits > 1 ? (int32_t)tiles : 0;
-        out.workspace_bytes = splits > 1 ? (uint64_t)splits * M * N * sizeof(float) : 0;
         if (debug_enabled())
             std::fprintf(stderr, "prefill dispatch G=%d M=%d N=%d K=%d cfg=%d occ=%d tiles=%d\n",
                          G, M, N, K, cfg, prefill_occupancy(cfg, *lim), out.grid);
@@ -466,6 +477,28 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
     *plan = out;
     return W4A16_OK;
 }
+
+namespace w4a16 {
+// A plan for the same prefill problem whose config needs no split-K scratch (every prefill config
+// gives the same bits): the wide tiles or the tiled kernel, which keep the canonical K segments
+// in registers, sized by M.  False when `in` is not a prefill plan.
+bool prefill_plan_no_scratch(const w4a16_plan& in, const w4a16_device_limits& lim, w4a16_plan* out) {
+    if (in.kernel < 1 || in.kernel > kNumPrefillTable) return false;
+    const int M = in.M, K = in.K;
+    static const int small_m[] = {2, 1, 4}, m64[] = {18, 3, 4}, m128[] = {20, 18, 4}, m256[] = {20, 7, 4},
+                     large_m[] = {24, 20, 7, 4};
+    const int* order = M <= 32 ? small_m : M <= 64 ? m64 : M <= 128 ? m128 : M <= 256 ? m256 : large_m;
+    const int n = order == large_m ? 4 : 3;
+    *out = in;
+    for (int i = 0; i < n; ++i) {
+        const int cfg = order[i];
+        if (kPrefillTable[cfg].kind <= 1 && prefill_occupancy(cfg, lim) > 0 && prefill_shape_ok(cfg, M, K) &&
+            fill_prefill_plan(cfg, out))
+            return true;
+    }
+    return false;
+}
+}  // namespace w4a16
 
 extern "C" int w4a16_query_device(int device, w4a16_device_limits* lim) {
     static std::mutex mu;

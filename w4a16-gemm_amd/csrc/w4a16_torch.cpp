@@ -61,11 +61,23 @@ void ensure_capture_pool(const at::Tensor& like) {
     if (!g_capture_pool.count(dev)) {
         at::Tensor buf = torch::zeros({kCapturePoolSlots}, like.options().dtype(torch::kInt32));
         // The zero fill runs on the current stream, and captured launches may later run on another
-        // one: wait for it here, once per device (never under capture: the caller checks).
-        TORCH_CHECK(hipStreamSynchronize(c10::hip::getCurrentHIPStream(dev).stream()) == hipSuccess,
-                    "w4a16_gemm: hipStreamSynchronize failed");
+        // one: wait for the fill alone, once per device, through an event (a stream or device
+        // synchronisation would invalidate a capture running on another stream in global mode).
+        hipEvent_t ev = nullptr;
+        TORCH_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess, "w4a16_gemm: hipEventCreate failed");
+        const bool ok = hipEventRecord(ev, c10::hip::getCurrentHIPStream(dev).stream()) == hipSuccess &&
+                        hipEventSynchronize(ev) == hipSuccess;
+        (void)hipEventDestroy(ev);
+        TORCH_CHECK(ok, "w4a16_gemm: waiting for the capture pool's zero fill failed");
         g_capture_pool[dev].buf = buf;
     }
+}
+
+// Test hook: forget the capture pool of a device, so that the next call under capture takes the
+// no-pool path (counters zeroed by a fill kernel recorded in the graph).
+void drop_capture_pool(int64_t device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_capture_pool.erase((int)device);
 }
 
 at::Tensor split_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
@@ -236,5 +248,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("quantize_pack", &w4a16_quantize_pack_t,
           "Group-wise RTN int4 quantisation + packing on the device: W [N, K] -> (Wp, scales)",
           py::arg("W"), py::arg("group_size"));
+    m.def("_debug_drop_capture_pool", &drop_capture_pool,
+          "Test hook: forget a device's capture pool (the next captured split-K call zeroes its own counters)",
+          py::arg("device") = 0);
     m.attr("abi_version") = w4a16_abi_version();
 }
