@@ -284,13 +284,21 @@ def bench_eager(torch, gemm, calls=240):
 
     dec_us, c1_us = device_us(seq), device_us(seq_c1)
     dec_host, c1_host = host_us(seq), host_us(seq_c1)
+    # where the host time of one call goes (C++ steady-clock timing inside the binding, configs[0])
+    import w4a16_opt
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(60e6))
+    parts = w4a16_opt._debug_host_breakdown(wc1[0][0], xc1, wc1[0][1], 200)
+    torch.cuda.synchronize()
+    parts = {k: round(v, 3) for k, v in parts.items()}
+    log(f"eager host breakdown (us per call): {parts}")
     log(f"eager: configs[1] {dec_us:.2f} us/call (host {dec_host:.2f}), configs[0] {c1_us:.2f} us/call "
         f"(host {c1_host:.2f})")
     step_bytes = sum(alg_bytes(M, N, K) for _, N, K, M in DECODE_CASES)
     return {"decode_us_per_call": round(dec_us, 3), "decode_GBps": round(step_bytes / 8 / dec_us / 1e3, 1),
             "decode_host_us_per_call": round(dec_host, 3),
             "c1_us_per_call": round(c1_us, 3), "c1_GBps": round(alg_bytes(c1M, c1N, c1K) / c1_us / 1e3, 1),
-            "c1_host_us_per_call": round(c1_host, 3),
+            "c1_host_us_per_call": round(c1_host, 3), "host_breakdown_us": parts,
             "method": f"{calls} eager w4a16_gemm calls back to back on the current stream (configs[1]: the 8 calls "
                       "in turn; configs[0]: one shape), weight copies > 2x Infinity Cache, HIP events; host = wall "
                       "time of the same Python loop while torch.cuda._sleep holds the GPU"}

@@ -443,7 +443,7 @@ __global__ void __launch_bounds__(WAVES * 64)
 decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
                    float* __restrict__ ws, int* __restrict__ counters,
-                   int M, int N, int K, int gshift, int splits, int kcw) {
+                   int M, int N, int K, int gshift, int splits, int kcw, int xcd_remap) {
     constexpr int S = D + 1;                                 // ring slots
     constexpr int WSLOT = NBW * 1024;                        // [n16 block][chunk][32 x 16 B]
     constexpr int XHI = XR == 16 ? 8 : 0;                    // shift of rows 8..15 (bank spread)
@@ -464,13 +464,15 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kb = lane >> 4;
     const int li = lane & 15;
-    // Workgroups are dealt to the 8 XCDs round-robin (b % 8).  Give each XCD a contiguous range of
-    // (tile, split) indices, so that neighbouring column tiles -- which share the 128-byte lines
-    // of every scale row -- meet in one L2.  A bijection: the results do not depend on it.  Without
-    // it the fetch from beyond L2 grows from 1.01-1.06x to 1.10-1.15x of the algorithmic bytes on
-    // the long-K shapes (each scale line is then fetched by several XCDs).
+    // Workgroups are dealt to the 8 XCDs round-robin (b % 8).  With xcd_remap, give each XCD a
+    // contiguous range of (tile, split) indices, so that neighbouring column tiles -- which share
+    // the 128-byte lines of every scale row -- meet in one L2.  A bijection: the results do not
+    // depend on it.  Without it the fetch from beyond L2 grows from 1.01-1.06x to 1.10-1.15x of
+    // the algorithmic bytes on the long-K shapes (each scale line is then fetched by several
+    // XCDs).  The host turns it off when the grid exceeds the CU count (gate/up, 448 workgroups):
+    // there the plain order was 0.1-0.3 us faster per call in alternating runs.
     const int nwg = gridDim.x;
-    const int bid = (nwg & 7) == 0 ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int bid = xcd_remap && (nwg & 7) == 0 ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
     const int split = bid % splits;
     const int tile = bid / splits;
     const int KC = K >> 6;
@@ -1291,9 +1293,13 @@ static hipError_t launch_decode_v(const w4a16_plan& p, const u4* Wp, const uint1
                            Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
     } else if constexpr (c.kind == 3) {
         const int xr = decode_ring_xr(p.M);
+        int dev = 0;
+        w4a16_device_limits lim{};
+        const int remap = hipGetDevice(&dev) == hipSuccess && w4a16_query_device(dev, &lim) == W4A16_OK
+                              ? (p.grid <= lim.cu_count ? 1 : 0) : 1;
 #define W4A16_RING(XR)                                                                                   \
         hipLaunchKernelGGL((decode_ring_kernel<c.nbw, c.waves, c.d, XR>), dim3(p.grid), dim3(c.waves * 64), \
-                           0, st, Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks)
+                           0, st, Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks, remap)
         // Shapes whose ring does not fit in LDS for a row count are never planned for it.
         if (xr == 1) {
             if constexpr (decode_lds_bytes(V, 1) <= 163840) W4A16_RING(1); else return hipErrorInvalidValue;

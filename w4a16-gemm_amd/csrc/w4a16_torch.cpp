@@ -13,7 +13,9 @@
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
+#include <chrono>
 #include <initializer_list>
+#include <vector>
 #include <map>
 #include <mutex>
 
@@ -163,6 +165,67 @@ torch::Tensor w4a16_gemm(torch::Tensor Wp, torch::Tensor x, torch::Tensor scales
     return y;
 }
 
+// Measurement hook (bench.py's eager leg): host microseconds per step of the eager call path,
+// each step timed over `reps` repetitions with the steady clock; the launches are real (the
+// caller synchronises afterwards).
+py::dict w4a16_host_breakdown(torch::Tensor Wp, torch::Tensor x, torch::Tensor scales, int64_t reps) {
+    using clk = std::chrono::steady_clock;
+    auto us = [&](clk::time_point a, clk::time_point b) {
+        return std::chrono::duration<double, std::micro>(b - a).count() / (double)reps;
+    };
+    w4a16_problem prob;
+    prob.M = x.size(0); prob.K = x.size(1); prob.N = scales.size(1); prob.groups = scales.size(0);
+    prob.wp_words = Wp.numel(); prob.Wp = Wp.data_ptr(); prob.x = x.data_ptr(); prob.scales = scales.data_ptr();
+    const int dev = x.device().index();
+    py::dict d;
+    auto t0 = clk::now();
+    for (int64_t i = 0; i < reps; ++i) {
+        TORCH_CHECK(Wp.is_cuda() && x.is_cuda() && scales.is_cuda(), "all tensors must be CUDA");
+        TORCH_CHECK(Wp.is_contiguous() && x.is_contiguous() && scales.is_contiguous(), "contiguous only");
+        const c10::DeviceGuard guard(x.device());
+    }
+    auto t1 = clk::now();
+    w4a16_device_limits lim{};
+    for (int64_t i = 0; i < reps; ++i) lim = limits_for(dev);
+    auto t2 = clk::now();
+    w4a16_plan plan;
+    char err[512];
+    for (int64_t i = 0; i < reps; ++i) TORCH_CHECK(w4a16_plan_create(&prob, -1, &lim, &plan, err, sizeof(err)) == W4A16_OK, err);
+    auto t3 = clk::now();
+    hipStream_t stream = nullptr;
+    for (int64_t i = 0; i < reps; ++i) stream = c10::hip::getCurrentHIPStream(dev).stream();
+    auto t4 = clk::now();
+    for (int64_t i = 0; i < reps; ++i) {                      // y from the caching allocator, freed again
+        torch::Tensor y = torch::empty({prob.M, prob.N}, x.options());
+        (void)y;
+    }
+    auto t5 = clk::now();
+    std::vector<torch::Tensor> ys;                            // outputs of the launch step (untimed)
+    ys.reserve(reps);
+    bool cap = false;
+    for (int64_t i = 0; i < reps; ++i) cap = cap || capturing(stream);
+    auto t6 = clk::now();
+    for (int64_t i = 0; i < reps; ++i) ensure_capture_pool(x);
+    auto t7a = clk::now();
+    for (int64_t i = 0; i < reps; ++i) ys.push_back(torch::empty({prob.M, prob.N}, x.options()));
+    auto t7 = clk::now();
+    TORCH_CHECK(plan.workspace_bytes == 0 && plan.counter_slots == 0, "host breakdown: unsplit plans only");
+    for (int64_t i = 0; i < reps; ++i)
+        TORCH_CHECK(w4a16_launch(&plan, static_cast<const int32_t*>(prob.Wp), static_cast<const uint16_t*>(prob.x),
+                                 static_cast<const uint16_t*>(prob.scales), reinterpret_cast<uint16_t*>(ys[i].data_ptr()),
+                                 nullptr, nullptr, stream) == W4A16_OK, "launch failed");
+    auto t8 = clk::now();
+    d["checks_and_device_guard"] = us(t0, t1);
+    d["device_limits"] = us(t1, t2);
+    d["plan_create"] = us(t2, t3);
+    d["current_stream"] = us(t3, t4);
+    d["allocate_y"] = us(t4, t5);
+    d["capture_check"] = us(t5, t6);
+    d["capture_pool_check"] = us(t6, t7a);
+    d["launch"] = us(t7, t8);
+    return d;
+}
+
 // Device quantise + pack: the GPU replacement of the reference's quantize_w4 followed by
 // pack_int4 (tests/quant.py:62-74, 34-48).  Returns (Wp int32 [N*K/8], scales fp16 [K/G, N]).
 std::tuple<torch::Tensor, torch::Tensor> w4a16_quantize_pack_t(torch::Tensor W, int64_t group_size) {
@@ -248,6 +311,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("quantize_pack", &w4a16_quantize_pack_t,
           "Group-wise RTN int4 quantisation + packing on the device: W [N, K] -> (Wp, scales)",
           py::arg("W"), py::arg("group_size"));
+    m.def("_debug_host_breakdown", &w4a16_host_breakdown,
+          "Measurement hook: host microseconds per step of an eager call (unsplit plans)",
+          py::arg("Wp"), py::arg("x"), py::arg("scales"), py::arg("reps") = 200);
     m.def("_debug_drop_capture_pool", &drop_capture_pool,
           "Test hook: forget a device's capture pool (the next captured split-K call zeroes its own counters)",
           py::arg("device") = 0);
