@@ -598,14 +598,16 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 #pragma unroll
             for (int b = 0; b < NBW; ++b) { bind_after_wait(wv[cc][b]); bind_after_wait(sc[cc][b]); }
         }
-        if constexpr (XR == 16) {
-            // 16 token rows: dequantise the whole pair first and pin the fragments ahead of the
-            // next step.  Left to the scheduler, the next step's vmcnt wait (an asm statement the
-            // arithmetic may move across) and its refill are hoisted above this pair's
-            // dequantisation, so the wave waits for pair p + 1 before computing pair p.  Pinned:
-            // 0.3-0.5 us per call faster on the down projection at M = 16, 0.1 on gate/up, in
-            // alternating runs; at 1 and 8 rows the same pin measured slower (gate/up M = 1
-            // +0.85 us), so the other row counts keep the scheduler's order.  Same MFMA sequence.
+        if constexpr (XR == 16 || NBW == 1) {
+            // Dequantise the whole pair first and pin the fragments ahead of the next step.  Left
+            // to the scheduler, the next step's vmcnt wait (an asm statement the arithmetic may
+            // move across) and its refill are hoisted above this pair's dequantisation, so the
+            // wave waits for pair p + 1 before computing pair p.  Pinned, in alternating runs:
+            // 16 rows 0.6 us per call faster on the down projection (M = 16), 0.2 on gate/up;
+            // single-block tiles 0.15-0.2 us faster (down M = 1, 4, 8).  Two- and four-block tiles
+            // at 1..8 rows measured slower pinned (gate/up M = 1 +0.85 us: with two pairs in
+            // flight the refill then waits for the compute), so they keep the scheduler's order.
+            // Same MFMA sequence either way.
             h8 af[2][NBW][2];
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
