@@ -72,6 +72,20 @@ def test_library_exports_every_declared_symbol(lib):
     assert lib.w4a16_abi_version() == 2
 
 
+def test_wave_stamps_only_in_the_instrumented_library(lib):
+    """The per-wave timestamps of wave_timeline.py live in libw4a16_hip_stamps.so (-DW4A16_WAVE_STAMPS);
+    the product library carries none of them and both export the same C ABI."""
+    assert not hasattr(lib, "w4a16_debug_wave_stamps")
+    stamps = os.path.join(ROOT, "w4a16-gemm_amd", "libw4a16_hip_stamps.so")
+    if not os.path.exists(stamps):
+        pytest.skip("libw4a16_hip_stamps.so not built (w4a16-gemm_amd/build.py)")
+    S = ctypes.CDLL(stamps)
+    assert hasattr(S, "w4a16_debug_wave_stamps") and hasattr(S, "w4a16_debug_wave_stamps_clear")
+    for n in re.findall(r"^\s*(?:int|int32_t|const char\*|void)\s+(w4a16_\w+)\s*\(", open(HEADER).read(), re.M):
+        assert hasattr(S, n), n
+    assert S.w4a16_abi_version() == lib.w4a16_abi_version()
+
+
 def test_plan_struct_layout_matches_header(lib):
     text = open(HEADER).read()
     body = text[text.index("typedef struct w4a16_plan"):text.index("} w4a16_plan;")]

@@ -9,6 +9,9 @@ Outputs (next to this file, git-ignored, shipped to the GPU box with the tree):
                                through an $ORIGIN rpath; import it as `w4a16_opt`.
   w4a16_ext<EXT_SUFFIX>        the same for the baseline GEMV module `w4a16_ext`.
   libw4a16_bwprobe.so          bandwidth probes of measure_bw.py.
+  libw4a16_hip_stamps.so       the same library built with -DW4A16_WAVE_STAMPS: the decode ring
+                               kernel records per-wave timestamps (wave_timeline.py); never
+                               loaded by the op, the tests' GEMM calls or bench.py.
 """
 from __future__ import annotations
 
@@ -83,6 +86,22 @@ def build_lib() -> str:
 
 
 PROBE = os.path.join(HERE, "libw4a16_bwprobe.so")
+STAMPS = os.path.join(HERE, "libw4a16_hip_stamps.so")
+
+
+def build_stamps() -> str:
+    """libw4a16_hip_stamps.so: the kernels file rebuilt with -DW4A16_WAVE_STAMPS, linked with the
+    other objects of build_lib (which must have run first)."""
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    objdir = os.path.join(HERE, "_build")
+    kobj = os.path.join(objdir, "w4a16_kernels_stamps.o")
+    _run([hipcc, *compile_flags("w4a16_kernels.hip"), "-DW4A16_WAVE_STAMPS", "-c",
+          os.path.join(CSRC, "w4a16_kernels.hip"), "-o", kobj])
+    objs = [kobj] + [os.path.join(objdir, src.rsplit(".", 1)[0] + ".o") for src, _ in SOURCES[1:]]
+    tmp = STAMPS + ".tmp"
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
+    os.replace(tmp, STAMPS)
+    return STAMPS
 
 
 def build_probe() -> str:
@@ -123,9 +142,12 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     build_lib()
     if not a.lib:
-        build_probe()
-        build_ext()
-        build_ext("w4a16_ext", "w4a16_ext_torch.cpp", EXT_GEMV)
+        with concurrent.futures.ThreadPoolExecutor(max_workers=2) as pool:
+            stamps = pool.submit(build_stamps)
+            build_probe()
+            build_ext()
+            build_ext("w4a16_ext", "w4a16_ext_torch.cpp", EXT_GEMV)
+            stamps.result()
     return 0
 
 

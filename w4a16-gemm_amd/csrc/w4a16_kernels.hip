@@ -403,6 +403,20 @@ decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
 }
 
+#ifdef W4A16_WAVE_STAMPS
+// Instrumented builds only (-DW4A16_WAVE_STAMPS: libw4a16_hip_stamps.so, built by build.py for
+// wave_timeline.py; the product library has none of this).  Lane 0 of every decode-ring wave
+// records the chip-wide 100 MHz clock (s_memrealtime) at kernel entry, after the prologue's loads
+// are issued, after its first pair is consumed, when its stream is done (before the cross-wave
+// reduction) and after its part of the output (y or partials) is written and acknowledged, plus
+// the wave's HW_ID and XCC_ID registers and its workgroup index: kStampWords words per wave,
+// indexed by blockIdx.x * WAVES + wave; waves past kStampWaves record nothing.
+constexpr int kStampWaves = 8192;
+constexpr int kStampWords = 8;
+__device__ uint32_t g_wave_stamps[kStampWaves * kStampWords];
+__device__ __forceinline__ uint32_t stamp_clock() { return (uint32_t)__builtin_amdgcn_s_memrealtime(); }
+#endif
+
 // Decode with a refill-ahead ring of chunk pairs (kind 3).
 //
 // Work split as in decode_stream_kernel: WAVES waves per column tile of NBW n16 blocks, each
@@ -464,6 +478,10 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kb = lane >> 4;
     const int li = lane & 15;
+#ifdef W4A16_WAVE_STAMPS
+    const uint32_t st_entry = stamp_clock();
+    uint32_t st_first = 0;
+#endif
     // Workgroups are dealt to the 8 XCDs round-robin (b % 8).  With xcd_remap, give each XCD a
     // contiguous range of (tile, split) indices, so that neighbouring column tiles -- which share
     // the 128-byte lines of every scale row -- meet in one L2.  A bijection: the results do not
@@ -653,6 +671,9 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // (< S) steady steps, then the last D pairs with shrinking waits.
     static_for<0, D>([&](auto s) { issue(s, s); });
     const int nsteady = npair - D;
+#ifdef W4A16_WAVE_STAMPS
+    const uint32_t st_issued = stamp_clock();
+#endif
     int p = 0;
     // Issue priority by progress.  A SIMD issues the oldest of its waves first, so of two waves
     // sharing a SIMD (8-wave workgroups, or two workgroups on one CU) the younger runs on the
@@ -669,6 +690,9 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
             if (p + T == phalf) __builtin_amdgcn_s_setprio(0);
             consume(p + T, t);
+#ifdef W4A16_WAVE_STAMPS
+            if (st_first == 0) st_first = stamp_clock();
+#endif
         });
     }
     __builtin_amdgcn_s_setprio(0);
@@ -679,14 +703,23 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             wait_vmcnt<(D - 1) * OPS>();
             issue(p + T + D, std::integral_constant<int, (T + D) % S>{});
             consume(p + T, t);
+#ifdef W4A16_WAVE_STAMPS
+            if (st_first == 0) st_first = stamp_clock();
+#endif
         });
         static_for<0, D>([&](auto t) {
             constexpr int T = decltype(t)::value;
             wait_vmcnt<(D - 1 - T) * OPS>();
             consume(p + R + T, std::integral_constant<int, (R + T) % S>{});
+#ifdef W4A16_WAVE_STAMPS
+            if (st_first == 0) st_first = stamp_clock();
+#endif
         });
     });
 
+#ifdef W4A16_WAVE_STAMPS
+    const uint32_t st_done = stamp_clock();
+#endif
     // Cross-wave reduction in wave order; each wave parks its tile at the start of its region
     // (its own loads are complete and its LDS reads have returned).
     f4* red = reinterpret_cast<f4*>(wreg);
@@ -701,6 +734,19 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         for (int w = 1; w < WAVES; ++w) sum += reinterpret_cast<const f4*>(wl + w * WAVE_BYTES)[rb * 64 + lane];
     }
     decode_finish<NBW, WAVES>(sum, tid < NBW * 64, rb, lane, split, tile, nb0, y, ws, counters, M, N, splits);
+#ifdef W4A16_WAVE_STAMPS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t st_stored = stamp_clock();
+    uint32_t hw_id, xcc_id;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_id));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_id));
+    const int gw = blockIdx.x * WAVES + wave;
+    if (lane == 0 && gw < kStampWaves) {
+        uint32_t* o = g_wave_stamps + (size_t)gw * kStampWords;
+        o[0] = st_entry; o[1] = st_issued; o[2] = st_first; o[3] = st_done;
+        o[4] = st_stored; o[5] = hw_id; o[6] = xcc_id; o[7] = blockIdx.x;
+    }
+#endif
 }
 
 // ----------------------------------------------------------------------------------- prefill
@@ -1591,3 +1637,21 @@ extern "C" int w4a16_debug_kernel_occupancy(int cfg) {
         default: return -1;
     }
 }
+
+#ifdef W4A16_WAVE_STAMPS
+// Instrumented builds only: copy out / clear the per-wave stamps of the decode ring kernel
+// (synchronous; call outside graph capture, after the launch has completed).
+extern "C" int w4a16_debug_wave_stamps(uint32_t* dst, int32_t max_waves) {
+    const int n = max_waves < w4a16::kStampWaves ? max_waves : w4a16::kStampWaves;
+    if (n <= 0 || !dst) return W4A16_ERR_INVALID;
+    if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(w4a16::g_wave_stamps), (size_t)n * w4a16::kStampWords * 4, 0,
+                            hipMemcpyDeviceToHost) != hipSuccess)
+        return W4A16_ERR_HIP;
+    return n;
+}
+extern "C" int w4a16_debug_wave_stamps_clear(void) {
+    static uint32_t zeros[w4a16::kStampWaves * w4a16::kStampWords];
+    return hipMemcpyToSymbol(HIP_SYMBOL(w4a16::g_wave_stamps), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice) ==
+                   hipSuccess ? W4A16_OK : W4A16_ERR_HIP;
+}
+#endif
