@@ -55,7 +55,7 @@ DECODE_CASES = [("gate_up", 14336, 4096, m) for m in (1, 4, 8, 16)] + \
                [("down", 4096, 14336, m) for m in (1, 4, 8, 16)]
 PREFILL_CASE = ("mlp70b", 28672, 8192, 2048)
 MODERATE_CASE = ("gate_up", 14336, 4096, 128, 64)          # M=128, G=64
-GRAPH_STEPS = 12                                             # decode steps captured per graph
+GRAPH_STEPS = 400                                            # longest timed region captured as one graph
 GEMV_CASES = [("c1_shape", 4096, 4096), ("gate_up", 14336, 4096)]    # (name, N, K) of w4a16_ext.w4a16_gemv
 C1_CASE = ("c1", 4096, 4096, 1)                              # M=1, K=N=4096, G=128
 G = 128
@@ -149,11 +149,14 @@ def bench_decode(torch, gemm, steps, warmup):
             x = xs[(name, M)]
             calls.append(lambda Wp=Wp, s=s, x=x: ys.append(gemm(Wp, x, s)))
         return calls
-    # One graph per step pays a graph-launch bubble (~8 us on this box) per 8 calls; like the
-    # reference benchmark (one graph over many calls), the steps are captured GRAPH_STEPS at a
-    # time, cycling through the copy phases, with single-step graphs for the remainder.
+    # Every graph launch pays a bubble (~8 us on this box, a tenth of a step); like the reference
+    # benchmark (one graph over many calls), the timed steps are captured as one graph of exactly
+    # `steps` steps (GRAPH_STEPS at a time beyond that), cycling through the copy phases, so the
+    # bubble is paid once per timed region whatever --steps is.  Single-step graphs serve the
+    # untimed warm-up steps.
+    per_big = min(steps, GRAPH_STEPS)
     singles = [graph_of(torch, step_calls(ph)) for ph in range(phases)]
-    big = graph_of(torch, [c for i in range(GRAPH_STEPS) for c in step_calls(i % phases)])
+    big = graph_of(torch, [c for i in range(per_big) for c in step_calls(i % phases)])
     # per-case timing (each case alone, rotating over all its copies)
     cases = []
     for name, N, K, M in DECODE_CASES:
@@ -169,14 +172,14 @@ def bench_decode(torch, gemm, steps, warmup):
                       "GBps": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                       "kernel": w4a16_opt.plan_info(M, N, K, G)["kernel_name"]})
         log(f"decode {name} M={M}: {us:.2f} us  {b / us / 1e3:.0f} GB/s")
-    ms = time_steps(torch, big, GRAPH_STEPS, singles, steps, warmup)
+    ms = time_steps(torch, big, per_big, singles, steps, warmup)
     step_bytes = sum(alg_bytes(M, N, K) for _, N, K, M in DECODE_CASES)
     ms_per_step = ms / steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     avg_launch_us = ms_per_step * 1e3 / len(DECODE_CASES)
     return {"value": value, "ms_per_step": ms_per_step, "step_bytes": step_bytes,
             "avg_launch_us": avg_launch_us, "bytes_per_launch": step_bytes / len(DECODE_CASES),
-            "cases": cases, "copies": copies}
+            "cases": cases, "copies": copies, "steps_per_graph": per_big}
 
 
 def bench_c1(torch, gemm, steps, warmup):
@@ -701,7 +704,7 @@ def main(argv=None) -> int:
             "vs_baseline": None, "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
             "config": {"workload": "BASELINE configs[1]: decode, Llama-3-8B MLP gate/up K=4096 N=14336 and down "
                                    "K=14336 N=4096, M in {1,4,8,16}, G=128; one step = the 8 calls",
-                       "G": G, "weight_copies_per_shape": dec["copies"], "timing": f"HIP graph replay ({GRAPH_STEPS} steps per graph), HIP events"},
+                       "G": G, "weight_copies_per_shape": dec["copies"], "timing": f"HIP graph replay ({dec['steps_per_graph']} steps per graph), HIP events"},
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4),
                          "kernel": " + ".join(sorted({c["kernel"] for c in dec["cases"]})),
