@@ -640,8 +640,9 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             }
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-                const h8 b0 = __builtin_bit_cast(h8, xv[cc][0]);
-                const h8 b1 = __builtin_bit_cast(h8, xv[cc][1]);
+                const u4 x0 = xv[cc][0], x1 = xv[cc][1];
+                const h8 b0 = __builtin_bit_cast(h8, x0);
+                const h8 b1 = __builtin_bit_cast(h8, x1);
 #pragma unroll
                 for (int b = 0; b < NBW; ++b) {
                     acc[b] = mfma16x16x32(af[cc][b][0], b0, acc[b]);
