@@ -68,15 +68,24 @@ def compile_flags(src: str) -> list[str]:
     return [*HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}"]
 
 
-def build_lib() -> str:
+STAMPS_OBJ = "w4a16_kernels_stamps.o"
+
+
+def build_lib(with_stamps: bool = False) -> str:
+    """libw4a16_hip.so; with_stamps also compiles the instrumented kernels object of
+    build_stamps in the same parallel pool (the two kernels files are the long poles)."""
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
     objs = [os.path.join(objdir, src.rsplit(".", 1)[0] + ".o") for src, _ in SOURCES]
+    cmds = [[hipcc, *compile_flags(src), "-c", os.path.join(CSRC, src), "-o", obj]
+            for (src, _), obj in zip(SOURCES, objs)]
+    if with_stamps:
+        cmds.insert(1, [hipcc, *compile_flags("w4a16_kernels.hip"), "-DW4A16_WAVE_STAMPS", "-c",
+                        os.path.join(CSRC, "w4a16_kernels.hip"), "-o", os.path.join(objdir, STAMPS_OBJ)])
     # the translation units compile independently: in parallel (the kernels file is the long pole)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        jobs = [pool.submit(_run, [hipcc, *compile_flags(src), "-c", os.path.join(CSRC, src), "-o", obj])
-                for (src, _), obj in zip(SOURCES, objs)]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+        jobs = [pool.submit(_run, cmd) for cmd in cmds]
         for job in jobs:
             job.result()
     tmp = LIB + ".tmp"
@@ -90,13 +99,11 @@ STAMPS = os.path.join(HERE, "libw4a16_hip_stamps.so")
 
 
 def build_stamps() -> str:
-    """libw4a16_hip_stamps.so: the kernels file rebuilt with -DW4A16_WAVE_STAMPS, linked with the
-    other objects of build_lib (which must have run first)."""
+    """libw4a16_hip_stamps.so: the kernels file built with -DW4A16_WAVE_STAMPS (by
+    build_lib(with_stamps=True), which must have run first), linked with build_lib's other objects."""
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     objdir = os.path.join(HERE, "_build")
-    kobj = os.path.join(objdir, "w4a16_kernels_stamps.o")
-    _run([hipcc, *compile_flags("w4a16_kernels.hip"), "-DW4A16_WAVE_STAMPS", "-c",
-          os.path.join(CSRC, "w4a16_kernels.hip"), "-o", kobj])
+    kobj = os.path.join(objdir, STAMPS_OBJ)
     objs = [kobj] + [os.path.join(objdir, src.rsplit(".", 1)[0] + ".o") for src, _ in SOURCES[1:]]
     tmp = STAMPS + ".tmp"
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
@@ -140,14 +147,13 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--lib", action="store_true", help="only build libw4a16_hip.so")
     a = ap.parse_args(argv)
-    build_lib()
+    build_lib(with_stamps=not a.lib)
     if not a.lib:
-        with concurrent.futures.ThreadPoolExecutor(max_workers=2) as pool:
-            stamps = pool.submit(build_stamps)
-            build_probe()
-            build_ext()
-            build_ext("w4a16_ext", "w4a16_ext_torch.cpp", EXT_GEMV)
-            stamps.result()
+        with concurrent.futures.ThreadPoolExecutor(max_workers=4) as pool:
+            jobs = [pool.submit(build_stamps), pool.submit(build_probe), pool.submit(build_ext),
+                    pool.submit(build_ext, "w4a16_ext", "w4a16_ext_torch.cpp", EXT_GEMV)]
+            for job in jobs:
+                job.result()
     return 0
 
 
