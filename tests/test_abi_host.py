@@ -84,6 +84,12 @@ def test_wave_stamps_only_in_the_instrumented_library(lib):
     for n in re.findall(r"^\s*(?:int|int32_t|const char\*|void)\s+(w4a16_\w+)\s*\(", open(HEADER).read(), re.M):
         assert hasattr(S, n), n
     assert S.w4a16_abi_version() == lib.w4a16_abi_version()
+    # argument checks, refused before any HIP call
+    S.w4a16_debug_wave_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+    buf = (ctypes.c_uint32 * 8)()
+    assert S.w4a16_debug_wave_stamps(buf, 0) == 1
+    assert S.w4a16_debug_wave_stamps(buf, 8193) == 1
+    assert S.w4a16_debug_wave_stamps(None, 1) == 1
 
 
 def test_plan_struct_layout_matches_header(lib):

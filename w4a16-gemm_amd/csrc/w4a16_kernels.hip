@@ -1640,15 +1640,15 @@ extern "C" int w4a16_debug_kernel_occupancy(int cfg) {
 }
 
 #ifdef W4A16_WAVE_STAMPS
-// Instrumented builds only: copy out / clear the per-wave stamps of the decode ring kernel
-// (synchronous; call outside graph capture, after the launch has completed).
-extern "C" int w4a16_debug_wave_stamps(uint32_t* dst, int32_t max_waves) {
-    const int n = max_waves < w4a16::kStampWaves ? max_waves : w4a16::kStampWaves;
-    if (n <= 0 || !dst) return W4A16_ERR_INVALID;
-    if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(w4a16::g_wave_stamps), (size_t)n * w4a16::kStampWords * 4, 0,
+// Instrumented builds only: copy out the stamps of the first `waves` waves (kStampWords words
+// each; at most kStampWaves) / clear them.  Synchronous: call outside graph capture, after the
+// launch has completed.  W4A16_OK, W4A16_ERR_INVALID or W4A16_ERR_HIP.
+extern "C" int w4a16_debug_wave_stamps(uint32_t* dst, int32_t waves) {
+    if (waves <= 0 || waves > w4a16::kStampWaves || !dst) return W4A16_ERR_INVALID;
+    if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(w4a16::g_wave_stamps), (size_t)waves * w4a16::kStampWords * 4, 0,
                             hipMemcpyDeviceToHost) != hipSuccess)
         return W4A16_ERR_HIP;
-    return n;
+    return W4A16_OK;
 }
 extern "C" int w4a16_debug_wave_stamps_clear(void) {
     static uint32_t zeros[w4a16::kStampWaves * w4a16::kStampWords];
