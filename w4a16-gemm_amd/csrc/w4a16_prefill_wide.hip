@@ -6,6 +6,8 @@
 // transfers per two chunks, which serialise the MFMA pipe); with this strategy every
 // accumulator stays in place in 128 AGPRs and the loop body is ~30% shorter.  The decode and
 // other prefill kernels keep the default scheduler (the strategy does not help them).
+// Kernel arguments: the first 16 dwords are preloaded into SGPRs (build.py), and the kernels take
+// what their prologue needs first (the grid size included, instead of gridDim.x), y last.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -63,8 +65,9 @@ namespace w4a16 {
 template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE, bool SEG, int R>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
-                    const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                    int M, int N, int K, int gshift, int tiles_m, int group_m, int seg_chunks) {
+                    const uint16_t* __restrict__ scales,
+                    int M, int N, int K, int gshift, int tiles_m, int group_m, int seg_chunks, int G,
+                    uint16_t* __restrict__ y) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M;
     constexpr int WN = BN / WAVES_N;
@@ -84,8 +87,7 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     const int kg = lane >> 5;
     const int r = lane & 31;
 
-    // XCD-aware tile order (a bijection on [0, gridDim.x)).
-    const int G = gridDim.x;
+    // XCD-aware tile order (a bijection on [0, G), G = gridDim.x).
     const int G8 = G >> 3;
     const int b = blockIdx.x;
     const int tile = b < (G8 << 3) ? (b & 7) * G8 + (b >> 3) : b;
@@ -330,8 +332,9 @@ prefill_wide_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 template <int BM, int BN, int WAVES_M, int WAVES_N, int WPE, bool SEG, int R>
 __global__ void __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 prefill_wide_pipe_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
-                         const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                         int M, int N, int K, int gshift, int tiles_m, int group_m, int seg_chunks) {
+                         const uint16_t* __restrict__ scales,
+                         int M, int N, int K, int gshift, int tiles_m, int group_m, int seg_chunks, int G,
+                         uint16_t* __restrict__ y) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M;
     constexpr int WN = BN / WAVES_N;
@@ -354,7 +357,6 @@ prefill_wide_pipe_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__
     const int r = lane & 31;
 
     // Tile order as in prefill_wide_kernel (XCD-contiguous, groups of group_m M tiles).
-    const int G = gridDim.x;
     const int G8 = G >> 3;
     const int b = blockIdx.x;
     const int tile = b < (G8 << 3) ? (b & 7) * G8 + (b >> 3) : b;
@@ -572,12 +574,12 @@ static void launch_wide_kernel(const w4a16_plan& p, const u4* Wp, const uint16_t
     constexpr int R = prefill_wide_steps(CFG, SEG);
     if constexpr (c.pipe)
         hipLaunchKernelGGL((prefill_wide_pipe_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, SEG, R>), dim3(p.grid),
-                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
-                           group_m, seg_chunks);
+                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, p.M, p.N, p.K, gshift, tiles_m,
+                           group_m, seg_chunks, p.grid, y);
     else
         hipLaunchKernelGGL((prefill_wide_kernel<c.bm, c.bn, c.waves_m, c.waves_n, c.wpe, SEG, R>), dim3(p.grid),
-                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, y, p.M, p.N, p.K, gshift, tiles_m,
-                           group_m, seg_chunks);
+                           dim3(c.waves_m * c.waves_n * 64), 0, st, Wp, x, s, p.M, p.N, p.K, gshift, tiles_m,
+                           group_m, seg_chunks, p.grid, y);
 }
 
 template <int CFG>
