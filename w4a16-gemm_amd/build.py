@@ -53,15 +53,15 @@ def _run(cmd: list[str]) -> None:
 # Sources of libw4a16_hip.so with their extra flags.  The wide prefill kernel is scheduled with
 # the max-memory-clause strategy: with the default strategy its 128 MFMA accumulators are rotated
 # through register copies inside the main loop (see the header of w4a16_prefill_wide.hip).  The
-# GEMM kernels' units preload the first 16 dwords of kernel arguments into SGPRs (gfx950 kernel
-# argument preloading; the compiler adds an entry that loads them itself where the firmware does
-# not preload), so the ring and wide kernels start their loads without an s_load round trip.
+# GEMM and GEMV kernels' units preload the first 16 dwords of kernel arguments into SGPRs (gfx950
+# kernel argument preloading; the compiler adds an entry that loads them itself where the firmware
+# does not preload), so the kernels start their loads without an s_load round trip.
 SOURCES = [
     ("w4a16_kernels.hip", ["-mllvm", "-amdgpu-kernarg-preload-count=16"]),
     ("w4a16_prefill_wide.hip", ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause",
                                 "-mllvm", "-amdgpu-kernarg-preload-count=16"]),
     ("w4a16_quantize.hip", []),
-    ("w4a16_gemv.hip", []),
+    ("w4a16_gemv.hip", ["-mllvm", "-amdgpu-kernarg-preload-count=16"]),
     ("w4a16_plan.cpp", []),
 ]
 
