@@ -199,9 +199,8 @@ __device__ __forceinline__ void prefill_tile_out(const f4 (&acc)[TM][NB], int m0
 template <int NBW, int WAVES, int D>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
-              const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-              float* __restrict__ ws, int* __restrict__ counters,
-              int M, int N, int K, int gshift, int splits, int kcw) {
+              const uint16_t* __restrict__ scales, int M, int N, int K, int gshift, int splits, int kcw,
+              uint16_t* __restrict__ y, float* __restrict__ ws, int* __restrict__ counters) {
     __shared__ __attribute__((aligned(16))) f4 red[WAVES][NBW][64];
 
     const int tid = threadIdx.x;
@@ -288,9 +287,8 @@ decode_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 template <int NBW, int WAVES, int D>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
-                     const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                     float* __restrict__ ws, int* __restrict__ counters,
-                     int M, int N, int K, int gshift, int splits, int kcw) {
+                     const uint16_t* __restrict__ scales, int M, int N, int K, int gshift, int splits, int kcw,
+                     uint16_t* __restrict__ y, float* __restrict__ ws, int* __restrict__ counters) {
     constexpr int SLOT = NBW * 1024;                         // [n16 block][2 chunks][512 B]
     constexpr int WAVE_BYTES = D * SLOT;
     constexpr int OPS = 4 + 2 * NBW + NBW;                   // x loads + scale loads + DMAs per pair
@@ -929,9 +927,8 @@ prefill_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 template <int TM, int D>
 __global__ void __launch_bounds__(64)
 prefill_stream_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
-                      const uint16_t* __restrict__ scales, uint16_t* __restrict__ y,
-                      int M, int N, int K, int gshift, float* __restrict__ ws, int* __restrict__ counters,
-                      int splits, int seg_pairs) {
+                      const uint16_t* __restrict__ scales, int M, int N, int K, int gshift, int splits,
+                      int seg_pairs, uint16_t* __restrict__ y, float* __restrict__ ws, int* __restrict__ counters) {
     constexpr int S = D + 1;                                 // ring slots
     constexpr int XD = 4 * TM;                               // x loads per pair (4 rows each)
     constexpr int SLOT = 1024 + XD * 1024 + 1024;            // weights, 16*TM rows x 256 B, scales
@@ -1330,7 +1327,7 @@ static hipError_t launch_prefill(const w4a16_plan& p, const u4* Wp, const uint16
                            seg_pairs, p.grid, y, ws, counters);
     else if constexpr (kPrefillTable[CFG].kind == 2)
         hipLaunchKernelGGL((prefill_stream_kernel<C::BM / 16, kPrefillTable[CFG].depth>), dim3(p.grid), dim3(64), 0, st,
-                           Wp, x, s, y, p.M, p.N, p.K, gshift, ws, counters, splits, seg_pairs);
+                           Wp, x, s, p.M, p.N, p.K, gshift, splits, seg_pairs, y, ws, counters);
     else if constexpr (kPrefillTable[CFG].kind == 1)
         return launch_prefill_wide(CFG, p, Wp, x, s, y, st);
     else
@@ -1374,10 +1371,10 @@ static hipError_t launch_decode_v(const w4a16_plan& p, const u4* Wp, const uint1
     const int gshift = p.G == 128 ? 1 : 0;
     if constexpr (c.kind == 0) {
         hipLaunchKernelGGL((decode_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
-                           Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
+                           Wp, x, s, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks, y, ws, cnt);
     } else if constexpr (c.kind == 2) {
         hipLaunchKernelGGL((decode_stream_kernel<c.nbw, c.waves, c.d>), dim3(p.grid), dim3(c.waves * 64), 0, st,
-                           Wp, x, s, y, ws, cnt, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks);
+                           Wp, x, s, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks, y, ws, cnt);
     } else if constexpr (c.kind == 3) {
         const int xr = decode_ring_xr(p.M);
         int dev = 0;
