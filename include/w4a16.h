@@ -121,9 +121,11 @@ int w4a16_launch(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
  * callers that cannot allocate device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  It allocates nothing (no hipMalloc, no allocating library
  * call); the caller passes only the inputs and y.  Runs on the current HIP device, on `stream`.
- * The first call on a device resolves the array's address and clears its counters with a small
- * kernel on `stream`; make that first call outside graph capture (under capture the clear would be
- * recorded into the graph instead of running now).  Later calls may be captured: the graph
+ * The first call on a device, whatever its plan, resolves the array's address, clears its counters
+ * with a small kernel on `stream` and launches a no-op kernel of the wide prefill code, so that the
+ * HIP runtime loads the library's GPU code then (it does so on a unit's first kernel launch, and
+ * that load allocates device memory); make that first call outside graph capture and before any
+ * region that must not allocate.  Later calls allocate nothing and may be captured: the graph
  * replays them against the same array.  Every call on one GPU shares that GPU's array: calls whose
  * plans have workspace_bytes > 0 must not overlap in time on one GPU (they race on the partials and
  * counters); plans without a workspace (unsplit prefill and decode) use no scratch.

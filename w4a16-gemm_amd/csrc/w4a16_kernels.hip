@@ -1279,6 +1279,7 @@ prefill_group_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
 hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
                                uint16_t* y, hipStream_t st);
 int prefill_wide_occupancy(int cfg);
+hipError_t prefill_wide_load_code(hipStream_t st);
 
 template <int CFG> struct PrefillCfg;
 #define W4A16_PREFILL_CFG(ID)                                                                  \
@@ -1443,8 +1444,11 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 char* g_scratch_ptr[kMaxScratchDevices];      // device address of `scratch` per device, or null
 
-// The device address of this device's scratch (resolved and cleared on first use), or null with
-// the message set.
+// The device address of this device's scratch, or null with the message set.  The first call on a
+// device resolves it, clears its counters and launches a no-op kernel of the wide prefill unit:
+// the HIP runtime loads a unit's GPU code (allocating device memory) on the first launch of one of
+// its kernels, and these two launches load both units a noalloc call can run, so later calls
+// allocate nothing.
 char* scratch_for_current_device(hipStream_t st) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
@@ -1462,7 +1466,8 @@ char* scratch_for_current_device(hipStream_t st) {
         constexpr int n16 = (int)(kScratchCounterBytes / 16);
         hipLaunchKernelGGL(scratch_clear_kernel, dim3((n16 + 255) / 256), dim3(256), 0, st,
                            static_cast<u4*>(ptr), n16);
-        const hipError_t le = hipGetLastError();
+        hipError_t le = hipGetLastError();
+        if (le == hipSuccess) le = prefill_wide_load_code(st);
         if (le != hipSuccess) {
             w4a16_set_last_error(hipGetErrorString(le));
             return nullptr;
@@ -1480,6 +1485,9 @@ int check_plan(const w4a16_plan& p);
 extern "C" int w4a16_launch_noalloc(const w4a16_plan* plan, const int32_t* Wp, const uint16_t* x,
                                     const uint16_t* scales, uint16_t* y, void* stream) {
     if (!plan) return W4A16_ERR_INVALID;
+    // Per-device set-up on the first call, whatever the plan (see scratch_for_current_device).
+    char* const scratch_base = scratch_for_current_device(reinterpret_cast<hipStream_t>(stream));
+    if (!scratch_base) return W4A16_ERR_HIP;
     // A prefill plan that needs more scratch than the static array (long K at moderate M splits
     // K over workgroups) runs as a scratch-free config of the same problem: every prefill config
     // gives the same bits.
@@ -1505,11 +1513,7 @@ extern "C" int w4a16_launch_noalloc(const w4a16_plan* plan, const int32_t* Wp, c
         w4a16_set_last_error(msg);
         return W4A16_ERR_WORKSPACE;
     }
-    char* base = nullptr;
-    if (plan->workspace_bytes || plan->counter_slots) {
-        base = scratch_for_current_device(reinterpret_cast<hipStream_t>(stream));
-        if (!base) return W4A16_ERR_HIP;
-    }
+    char* const base = plan->workspace_bytes || plan->counter_slots ? scratch_base : nullptr;
     return w4a16_launch(plan, Wp, x, scales, y, base ? base + kScratchCounterBytes : nullptr,
                         base ? reinterpret_cast<int32_t*>(base) : nullptr, stream);
 }

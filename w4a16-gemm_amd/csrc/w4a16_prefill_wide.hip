@@ -607,6 +607,16 @@ static hipError_t launch_wide(const w4a16_plan& p, const u4* Wp, const uint16_t*
     return hipGetLastError();
 }
 
+// A kernel that does nothing.  The HIP runtime loads each unit's GPU code on the first launch of
+// one of its kernels, and that load allocates device memory; w4a16_launch_noalloc launches this
+// once per device in its first call, so that its later calls running wide configs allocate nothing.
+__global__ void __launch_bounds__(64) wide_unit_load_kernel() {}
+
+hipError_t prefill_wide_load_code(hipStream_t st) {
+    hipLaunchKernelGGL(wide_unit_load_kernel, dim3(1), dim3(64), 0, st);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_wide(int cfg, const w4a16_plan& p, const u4* Wp, const uint16_t* x, const uint16_t* s,
                                uint16_t* y, hipStream_t st) {
     switch (cfg) {
