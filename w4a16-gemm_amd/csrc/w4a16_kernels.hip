@@ -627,8 +627,8 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             // wave waits for pair p + 1 before computing pair p.  Pinned, in alternating runs:
             // 16 rows 0.6 us per call faster on the down projection (M = 16), 0.2 on gate/up;
             // single-block tiles 0.15-0.2 us faster (down M = 1, 4, 8).  Two- and four-block tiles
-            // at 1..8 rows measured slower pinned (gate/up M = 1 +0.85 us: with two pairs in
-            // flight the refill then waits for the compute), so they keep the scheduler's order.
+            // at 1..8 rows measured slower with the whole pair pinned (gate/up M = 1 +0.85 us: with
+            // two pairs in flight the refill then waits for all the compute); see the half pin below.
             // Same MFMA sequence either way.
             h8 af[2][NBW][2];
 #pragma unroll
@@ -654,6 +654,12 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                 }
             }
         } else {
+            // Half pin at 1 and 8 rows: only the pair's first chunk is dequantised ahead of the
+            // next step, so the refill waits for half the compute instead of all of it.  In
+            // alternating runs on two boxes: gate/up M = 1 0.24-0.27 us per call faster, M = 8
+            // 0.08; at 4 rows it measured 0.12 faster on one box and 0.24 slower on the other,
+            // so 4 rows keep the scheduler's order.
+            constexpr bool pin_first = XR == 1 || XR == 8;
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const u4 x0 = xv[cc][0], x1 = xv[cc][1];
@@ -663,8 +669,18 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                 for (int b = 0; b < NBW; ++b) {
                     const h2 s2 = scale2((uint16_t)sc[cc][b]);
                     const u4 w = wv[cc][b];
-                    acc[b] = mfma16x16x32(dq_frag(w.x, w.y, d, s2), b0, acc[b]);
-                    acc[b] = mfma16x16x32(dq_frag(w.z, w.w, d, s2), b1, acc[b]);
+                    if constexpr (pin_first) {
+                        const h8 a0 = dq_frag(w.x, w.y, d, s2);
+                        const h8 a1 = dq_frag(w.z, w.w, d, s2);
+                        if (cc == 0) asm volatile("" ::"v"(a0), "v"(a1));
+                        acc[b] = mfma16x16x32(a0, b0, acc[b]);
+                        acc[b] = mfma16x16x32(a1, b1, acc[b]);
+                    } else {
+                        // (This expression form fixes the scheduler's starting order; naming
+                        // the fragments first, unpinned, compiles to a different schedule.)
+                        acc[b] = mfma16x16x32(dq_frag(w.x, w.y, d, s2), b0, acc[b]);
+                        acc[b] = mfma16x16x32(dq_frag(w.z, w.w, d, s2), b1, acc[b]);
+                    }
                 }
             }
         }
