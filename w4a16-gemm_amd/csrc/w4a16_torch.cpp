@@ -76,10 +76,16 @@ void ensure_capture_pool(const at::Tensor& like) {
 }
 
 // Test hook: forget the capture pool of a device, so that the next call under capture takes the
-// no-pool path (counters zeroed by a fill kernel recorded in the graph).
+// no-pool path (counters zeroed by a fill kernel recorded in the graph).  The dropped buffer is
+// kept alive: graphs captured before the drop hold pointers into it and may still be replayed.
+std::vector<at::Tensor> g_dropped_pools;
+
 void drop_capture_pool(int64_t device) {
     std::lock_guard<std::mutex> lk(g_mu);
-    g_capture_pool.erase((int)device);
+    auto it = g_capture_pool.find((int)device);
+    if (it == g_capture_pool.end()) return;
+    g_dropped_pools.push_back(it->second.buf);
+    g_capture_pool.erase(it);
 }
 
 at::Tensor split_counters(const at::Tensor& like, hipStream_t stream, int32_t slots) {
