@@ -533,6 +533,42 @@ def test_wide_configs_refused_where_32bit_offsets_wrap(lib, monkeypatch, cfg):
         assert chosen_bm is None or _wide_offsets_fit(chosen_bm, K), (cfg, K, p.kernel)
 
 
+# Waves of the refill-ahead ring shapes (kind 3) of the decode table (w4a16_internal.h,
+# kDecodeTable ids 16..31).  Those of 8 or more waves address x with 32-bit per-lane byte offsets
+# of up to 15 token rows (15 * K * 2 + 256 bytes from a 64-bit base), so the planner keeps them
+# to K < 2^27.
+RING_WAVES = {16: 4, 17: 4, 18: 8, 19: 8, 20: 4, 21: 4, 22: 8, 23: 4, 24: 16, 25: 8, 26: 8, 27: 16, 28: 4, 29: 8,
+              30: 16, 31: 8}
+
+
+def test_wide_decode_rings_refused_where_32bit_x_offsets_wrap(lib, monkeypatch):
+    assert 15 * (2**27) * 2 + 256 < 2**32 < 15 * (2**28) * 2
+    taken = 0
+    for K in (2**27 - 4096, 2**27, 2**27 + 4096):
+        for M in (1, 4, 16):
+            rc, p, err = plan(lib, M=M, N=64, K=K, G=128)
+            assert rc == 0 and p.kernel == 0, err
+            assert _check(lib, p) == 0
+            if K >= 2**27:
+                assert RING_WAVES.get(p.decode_variant, 0) < 8, (K, M, p.decode_variant)
+            for v, waves in RING_WAVES.items():
+                if waves < 8:
+                    continue
+                monkeypatch.setenv("W4A16_DECODE", f"{v},1")
+                rc, p, err = plan(lib, M=M, N=64, K=K, G=128)
+                assert rc == 0 and _check(lib, p) == 0, err
+                if K >= 2**27:
+                    assert p.decode_variant != v, (K, M, v)
+                elif p.decode_variant == v:               # taken below the bound (LDS permitting)
+                    taken += 1
+                    q = Plan.from_buffer_copy(p)          # the same plan moved past the bound
+                    q.K = 2**27
+                    q.slab_chunks = (2**27 // 64) // waves
+                    assert _check(lib, q) == 1, (M, v)
+                monkeypatch.delenv("W4A16_DECODE")
+    assert taken >= 6
+
+
 def test_auto_plan_at_k_beyond_the_256_row_wide_tiles(lib):
     """K = 2^23 + 2^16: the 256-row wide tiles (configs 6, 21) would wrap their x offsets; the auto
     plan takes a config whose addresses fit, and passes the launch-side check."""

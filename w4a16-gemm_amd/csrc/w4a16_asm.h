@@ -114,4 +114,19 @@ __device__ __forceinline__ uint32_t gload_u16_sbase(const void* base, uint32_t o
     return v;
 }
 
+// Direct-to-LDS loads with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte offset:
+// lane i's bytes land at LDS address lds + i * size.  The address arithmetic stays in SALU (the
+// builtin takes a 64-bit per-lane pointer, one VALU add per load).  The compiler writes M0, the
+// LDS address, for the "{m0}" operand; the s_nop is the wait state an M0 write needs before an
+// LDS DMA.  The loads count in vmcnt like any other; the caller waits for them explicitly.
+__device__ __forceinline__ void dma16_sbase_nt(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma16_sbase(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4_sbase(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
 }  // namespace w4a16

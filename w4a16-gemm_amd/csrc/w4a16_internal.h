@@ -171,13 +171,16 @@ constexpr int decode_lds_bytes(int v, int M) {
                                               (decode_ring_xr(M) == 16 ? 16 : 0)) + 16;
 }
 // Whether a decode shape can cover K (in 64-wide chunks, group size G) with `splits` workgroups
-// per column tile.
+// per column tile.  The 8- and 16-wave rings address x with 32-bit per-lane byte offsets of up to
+// 15 rows (15 * K * 2 + 256 bytes), so they take K < 2^27 (KC < 2^21).
+constexpr int kDecodeRingSbaseMaxKC = 1 << 21;
 constexpr bool decode_shape_fits(int v, int KC, int splits, int G) {
     return splits >= 1 && KC % (splits * kDecodeTable[v].waves) == 0 &&
            (kDecodeTable[v].kind != 2 || ((KC / (splits * kDecodeTable[v].waves)) % (2 * kDecodeTable[v].d) == 0)) &&
            (kDecodeTable[v].kind != 3 ||
             ((KC / (splits * kDecodeTable[v].waves)) % 2 == 0 &&
-             KC / (splits * kDecodeTable[v].waves) >= 2 * kDecodeTable[v].d));
+             KC / (splits * kDecodeTable[v].waves) >= 2 * kDecodeTable[v].d &&
+             (kDecodeTable[v].waves < 8 || KC < kDecodeRingSbaseMaxKC)));
 }
 
 // Counter buffer size (ints) the library may ask for: one per decode column tile.

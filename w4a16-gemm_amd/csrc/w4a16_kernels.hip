@@ -537,28 +537,69 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
             xsrc[q] = reinterpret_cast<const char*>(x + (size_t)min(r, M - 1) * K + (size_t)kc0 * 64 + gseg * 8);
         }
     }
-    auto issue = [&](int p, auto slot) {
-        char* sl = wreg + decltype(slot)::value * SLOT;
+    // The same sources as a wave-uniform base plus a 32-bit lane offset, for the 8- and 16-wave
+    // rings (SGPR-base DMAs below).  kc0 is even (the chunks per wave are), so the scale row of
+    // chunk kc0 + cc is (kc0 >> gshift) + (cc >> gshift), cc = se / (2 * NBW) in {0, 1}.  The x
+    // offset is below 15 * K * 2 + 256 bytes: decode_shape_fits keeps K < 2^27 for these rings.
+    const char* sbase_g = reinterpret_cast<const char*>(scales + (size_t)(kc0 >> gshift) * N + (size_t)nb0 * 16);
+    const uint32_t soff_g = (uint32_t)((((se / (2 * NBW)) >> gshift) * N + ((se >> 1) % NBW) * 16 + (se & 1) * 8) * 2);
+    const char* xbase_g = reinterpret_cast<const char*>(x) + (size_t)kc0 * 128;
+    uint32_t xoff_g[XD];
+    if constexpr (XR == 1) {
+        const int u = lane >> 2;
+        xoff_g[0] = (uint32_t)((32 * (u >> 3) + 16 * ((u >> 2) & 1) + 4 * (lane & 3) + (u & 3)) * 4);
+    } else {
 #pragma unroll
-        for (int b = 0; b < NBW; ++b)
-            __builtin_amdgcn_global_load_lds((const void*)(wbase_g + (size_t)b * KC * 512 + (size_t)p * (1024 * WAVES) + woff_g),
-                                             (__attribute__((address_space(3))) void*)(sl + b * 1024), 16, 0,
-                                             kWeightStreamPolicy);
-        if constexpr (XR == 1) {
-            __builtin_amdgcn_global_load_lds((const void*)(xsrc[0] + (size_t)p * (256 * WAVES)),
-                                             (__attribute__((address_space(3))) void*)(sl + WSLOT), 4, 0, 0);
-        } else {
-#pragma unroll
-            for (int q = 0; q < XD; ++q)
-                __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * (256 * WAVES)),
-                                                 (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024 +
-                                                                                           (q >= 2 ? XHI : 0)),
-                                                 16, 0, 0);
+        for (int q = 0; q < XD; ++q) {
+            const int r = (64 * q + lane) >> 4;
+            const int gseg = (lane & 15) ^ (r & 7);
+            xoff_g[q] = (uint32_t)min(r, M - 1) * (uint32_t)K * 2u + (uint32_t)gseg * 16u;
         }
-        if (lane < 4 * NBW)
-            __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)p * (sstep * WAVES)),
-                                             (__attribute__((address_space(3))) void*)(sl + SCOFF), 16, 0, 0);
-        asm volatile("" ::: "memory");
+    }
+    // One pair's loads into ring slot `slot`.  The 8- and 16-wave rings issue them through asm with
+    // SGPR bases, which keeps the per-pair address arithmetic out of the VALU (the dequantisation
+    // already keeps the VALU busy); in alternating runs on two boxes: gate/up M = 16 0.22-0.24 us
+    // per call faster, down M = 1, 4, 8 0.03-0.13 us, the 70B MLP shapes 0.7-4.7%, configs[0]
+    // 0.02 us slower.  The 4-wave rings measured level to 1.2% slower that way and keep the
+    // builtin (64-bit per-lane pointers).
+    auto issue = [&](int p, auto slot) {
+        if constexpr (WAVES >= 8) {
+            const uint32_t sl = lds_wave + decltype(slot)::value * SLOT;
+#pragma unroll
+            for (int b = 0; b < NBW; ++b)
+                dma16_sbase_nt(wbase_g + (size_t)b * KC * 512 + (size_t)p * (1024 * WAVES), woff_g, sl + b * 1024);
+            if constexpr (XR == 1) {
+                dma4_sbase(xbase_g + (size_t)p * (256 * WAVES), xoff_g[0], sl + WSLOT);
+            } else {
+#pragma unroll
+                for (int q = 0; q < XD; ++q)
+                    dma16_sbase(xbase_g + (size_t)p * (256 * WAVES), xoff_g[q], sl + WSLOT + q * 1024 + (q >= 2 ? XHI : 0));
+            }
+            if (lane < 4 * NBW)
+                dma16_sbase(sbase_g + (size_t)p * (sstep * WAVES), soff_g, sl + SCOFF);
+        } else {
+            char* sl = wreg + decltype(slot)::value * SLOT;
+#pragma unroll
+            for (int b = 0; b < NBW; ++b)
+                __builtin_amdgcn_global_load_lds((const void*)(wbase_g + (size_t)b * KC * 512 + (size_t)p * (1024 * WAVES) + woff_g),
+                                                 (__attribute__((address_space(3))) void*)(sl + b * 1024), 16, 0,
+                                                 kWeightStreamPolicy);
+            if constexpr (XR == 1) {
+                __builtin_amdgcn_global_load_lds((const void*)(xsrc[0] + (size_t)p * (256 * WAVES)),
+                                                 (__attribute__((address_space(3))) void*)(sl + WSLOT), 4, 0, 0);
+            } else {
+#pragma unroll
+                for (int q = 0; q < XD; ++q)
+                    __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + (size_t)p * (256 * WAVES)),
+                                                     (__attribute__((address_space(3))) void*)(sl + WSLOT + q * 1024 +
+                                                                                               (q >= 2 ? XHI : 0)),
+                                                     16, 0, 0);
+            }
+            if (lane < 4 * NBW)
+                __builtin_amdgcn_global_load_lds((const void*)(ssrc + (size_t)p * (sstep * WAVES)),
+                                                 (__attribute__((address_space(3))) void*)(sl + SCOFF), 16, 0, 0);
+            asm volatile("" ::: "memory");
+        }
     };
 
     // Per-lane LDS bases (slot 0).  x, XR >= 4: global segment 8*cc + 4*h + c of row xr sits at
