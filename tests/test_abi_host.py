@@ -353,7 +353,8 @@ def test_gcn_arch_name_parse(lib, name, want):
 
 
 @pytest.mark.parametrize("M,N,K,want", [
-    (1, 14336, 4096, (20, 1)), (4, 14336, 4096, (20, 1)), (8, 14336, 4096, (20, 1)), (16, 14336, 4096, (18, 1)),
+    (1, 14336, 4096, (20, 1)), (4, 14336, 4096, (20, 1)), (6, 14336, 4096, (20, 1)), (7, 14336, 4096, (18, 1)),
+    (8, 14336, 4096, (18, 1)), (16, 14336, 4096, (18, 1)), (8, 18944, 3584, (20, 1)),
     (1, 4096, 14336, (29, 1)), (4, 4096, 14336, (29, 1)), (8, 4096, 14336, (19, 1)), (16, 4096, 14336, (20, 2)),
     (1, 28672, 4096, (21, 1)), (4, 28672, 4096, (21, 1)),                    # fused gate/up: twice as wide
     (1, 10240, 8192, (29, 1)), (4, 10240, 8192, (19, 1)), (8, 10240, 8192, (31, 1)),  # 70B qkv: K = 8192, 640 blocks

@@ -321,10 +321,12 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             // w4a16-gemm_amd/route_sweep.py) for the Llama-3 decode projections, tried in order;
             // the first that fits wins:
             //  * N alone fills the device with 4-block tiles (gate/up, N = 14336): refill-ahead
-            //    rings of 4 waves, 2 blocks while the x rows are few (M <= 8: M = 8, 9.51 vs
-            //    9.88 us), else 4 blocks on 8 waves with one pair in flight each (M = 16: 9.42-9.48
-            //    vs 9.75-9.81 us for 4 waves with two pairs, three alternating runs; 10.05 vs 11.16
-            //    for 2 blocks); no split.  Twice as wide (fused gate/up, N = 28672): single-block rings
+            //    rings of 4 waves, 2 blocks while the x rows are few (M <= 6), else 4 blocks on 8
+            //    waves with one pair in flight each (M = 16: 9.42-9.48 vs 9.75-9.81 us for 4 waves
+            //    with two pairs, three alternating runs; 10.05 vs 11.16 for 2 blocks; since the
+            //    8-wave rings issue their DMAs with SGPR bases, also M = 7, 8: M = 8 8.48-8.54 vs
+            //    8.70-8.79 us on two boxes, M = 7 8.50 vs 8.59, while M = 5, 6 stay 0.06-0.11 us
+            //    faster on 2 blocks); no split.  Twice as wide (fused gate/up, N = 28672): single-block rings
             //    of 4 waves with 4 pairs in flight at M <= 4 (M = 1 in four sweeps at K = 4096 and 8192:
             //    14.27-15.05 vs 15.15-15.33 us and 25.69-25.86 vs 25.83-27.58 for 8 waves with 3 pairs);
             //  * long K, moderate N (down, K = 14336): single-block refill-ahead rings of 8 waves,
@@ -355,6 +357,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             Cand vwide_small_m[] = {{21, 1}, {20, 1}, {12, 1}};
             Cand wide_small_m[] = {{20, 1}, {12, 1}, {7, 1}};
             Cand wide[] = {{16, 1}, {12, 1}, {7, 1}};
+            Cand wide_mid_m[] = {{18, 1}, {20, 1}, {12, 1}};
             Cand wide_large_m[] = {{18, 1}, {16, 1}, {12, 1}};
             Cand longk_m4[] = {{29, 1}, {19, 1}, {22, 2}};
             Cand longk_small_m[] = {{19, 1}, {22, 2}, {22, 2}};
@@ -383,7 +386,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus && very_wide)
                 list = M <= 1 ? vwide_m1 : M <= 4 ? vwide_small_m : wide;
             else if ((int64_t)ntiles_of(12) * 8 >= 7LL * cus)
-                list = M <= 8 ? wide_small_m : wide_large_m;
+                list = M <= 6 ? wide_small_m : M <= 8 ? wide_mid_m : wide_large_m;
             else if (KC == 128 && many_blocks && ntiles_of(26) <= cus)
                 list = M <= 8 ? k8k_fit_small_m : k8k_fit_large_m;
             else if (KC == 128 && many_blocks)
