@@ -562,6 +562,7 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // per call faster, down M = 1, 4, 8 0.03-0.13 us, the 70B MLP shapes 0.7-4.7%, configs[0]
     // 0.02 us slower.  The 4-wave rings measured level to 1.2% slower that way and keep the
     // builtin (64-bit per-lane pointers).
+    static_assert(kWeightStreamPolicy == 2, "the asm weight DMAs below are written with the nt policy");
     auto issue = [&](int p, auto slot) {
         if constexpr (WAVES >= 8) {
             const uint32_t sl = lds_wave + decltype(slot)::value * SLOT;
