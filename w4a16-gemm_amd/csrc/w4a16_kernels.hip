@@ -698,9 +698,9 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
         } else {
             // Half pin at 1 and 8 rows: only the pair's first chunk is dequantised ahead of the
             // next step, so the refill waits for half the compute instead of all of it.  In
-            // alternating runs on two boxes: gate/up M = 1 0.24-0.27 us per call faster, M = 8
-            // 0.08; at 4 rows it measured 0.12 faster on one box and 0.24 slower on the other,
-            // so 4 rows keep the scheduler's order.
+            // alternating runs: gate/up M = 1 0.17-0.27 us per call faster (three boxes), M = 8
+            // 0.14 on the four-block 8-wave ring (order-rotated runs); at 4 rows it measured 0.12
+            // faster on one box and 0.24 slower on another, so 4 rows keep the scheduler's order.
             constexpr bool pin_first = XR == 1 || XR == 8;
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
