@@ -696,12 +696,11 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                 }
             }
         } else {
-            // Half pin at 1 and 8 rows: only the pair's first chunk is dequantised ahead of the
-            // next step, so the refill waits for half the compute instead of all of it.  In
-            // alternating runs: gate/up M = 1 0.17-0.27 us per call faster (three boxes), M = 8
-            // 0.14 on the four-block 8-wave ring (order-rotated runs); at 4 rows it measured 0.12
-            // faster on one box and 0.24 slower on another, so 4 rows keep the scheduler's order.
-            constexpr bool pin_first = XR == 1 || XR == 8;
+            // Half pin (multi-block tiles at 1, 4 and 8 rows): only the pair's first chunk is
+            // dequantised ahead of the next step, so the refill waits for half the compute instead
+            // of all of it.  In alternating runs: gate/up M = 1 0.17-0.27 us per call faster (three
+            // boxes), M = 8 0.14 on the four-block 8-wave ring; M = 4 0.13-0.14 (gate/up and qkv, in
+            // three order-rotated runs; one earlier run without rotation read it 0.24 slower).
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const u4 x0 = xv[cc][0], x1 = xv[cc][1];
@@ -711,18 +710,11 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                 for (int b = 0; b < NBW; ++b) {
                     const h2 s2 = scale2((uint16_t)sc[cc][b]);
                     const u4 w = wv[cc][b];
-                    if constexpr (pin_first) {
-                        const h8 a0 = dq_frag(w.x, w.y, d, s2);
-                        const h8 a1 = dq_frag(w.z, w.w, d, s2);
-                        if (cc == 0) asm volatile("" ::"v"(a0), "v"(a1));
-                        acc[b] = mfma16x16x32(a0, b0, acc[b]);
-                        acc[b] = mfma16x16x32(a1, b1, acc[b]);
-                    } else {
-                        // (This expression form fixes the scheduler's starting order; naming
-                        // the fragments first, unpinned, compiles to a different schedule.)
-                        acc[b] = mfma16x16x32(dq_frag(w.x, w.y, d, s2), b0, acc[b]);
-                        acc[b] = mfma16x16x32(dq_frag(w.z, w.w, d, s2), b1, acc[b]);
-                    }
+                    const h8 a0 = dq_frag(w.x, w.y, d, s2);
+                    const h8 a1 = dq_frag(w.z, w.w, d, s2);
+                    if (cc == 0) asm volatile("" ::"v"(a0), "v"(a1));
+                    acc[b] = mfma16x16x32(a0, b0, acc[b]);
+                    acc[b] = mfma16x16x32(a1, b1, acc[b]);
                 }
             }
         }
