@@ -696,11 +696,15 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                 }
             }
         } else {
-            // Half pin (multi-block tiles at 1, 4 and 8 rows): only the pair's first chunk is
-            // dequantised ahead of the next step, so the refill waits for half the compute instead
-            // of all of it.  In alternating runs: gate/up M = 1 0.17-0.27 us per call faster (three
-            // boxes), M = 8 0.14 on the four-block 8-wave ring; M = 4 0.13-0.14 (gate/up and qkv, in
-            // three order-rotated runs; one earlier run without rotation read it 0.24 slower).
+            // Partial pin (multi-block tiles at 1, 4 and 8 rows): part of the pair is dequantised
+            // ahead of the next step, so the refill waits for that part of the compute instead of
+            // all of it -- the first chunk of two-block tiles (half the pair), the first block of
+            // four-block tiles (a quarter).  In alternating runs against no pin: gate/up M = 1
+            // 0.17-0.27 us per call faster (three boxes), M = 4 0.13-0.14 (gate/up and qkv, three
+            // order-rotated runs; one earlier run without rotation read it 0.24 slower), M = 8 on the
+            // four-block ring 0.14 with the first chunk pinned and another 0.15 with the first block
+            // instead (order-rotated, two boxes; on two-block tiles the first block measured
+            // -0.03..-0.06 at gate/up M = 1, 4 and +0.04 at qkv M = 4, so they keep the chunk).
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const u4 x0 = xv[cc][0], x1 = xv[cc][1];
@@ -712,7 +716,7 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
                     const u4 w = wv[cc][b];
                     const h8 a0 = dq_frag(w.x, w.y, d, s2);
                     const h8 a1 = dq_frag(w.z, w.w, d, s2);
-                    if (cc == 0) asm volatile("" ::"v"(a0), "v"(a1));
+                    if (NBW >= 4 ? b == 0 : cc == 0) asm volatile("" ::"v"(a0), "v"(a1));
                     acc[b] = mfma16x16x32(a0, b0, acc[b]);
                     acc[b] = mfma16x16x32(a1, b1, acc[b]);
                 }
