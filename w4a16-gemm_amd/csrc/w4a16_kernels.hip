@@ -493,7 +493,10 @@ decode_ring_kernel(const u4* __restrict__ Wp, const uint16_t* __restrict__ x,
     // depend on it.  Without it the fetch from beyond L2 grows from 1.01-1.06x to 1.10-1.15x of
     // the algorithmic bytes on the long-K shapes (each scale line is then fetched by several
     // XCDs).  The host turns it off when the grid exceeds the CU count (gate/up, 448 workgroups):
-    // there the plain order was 0.1-0.3 us faster per call in alternating runs.
+    // there the plain order was 0.1-0.3 us faster per call in alternating runs; and for four-block
+    // tiles at K <= 4096 (gate/up M = 7..16, 224 workgroups: M = 8 0.06-0.27 us and M = 16
+    // 0.10-0.24 us faster plain, order-rotated runs on three boxes), while four-block tiles at
+    // K = 8192 measured 0.14-0.24 us slower plain and narrower tiles at K = 4096 level.
     const int bid = xcd_remap && (nwg & 7) == 0 ? (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3) : blockIdx.x;
     const int split = bid % splits;
     const int tile = bid / splits;
@@ -1446,7 +1449,7 @@ static hipError_t launch_decode_v(const w4a16_plan& p, const u4* Wp, const uint1
         int dev = 0;
         w4a16_device_limits lim{};
         const int remap = hipGetDevice(&dev) == hipSuccess && w4a16_query_device(dev, &lim) == W4A16_OK
-                              ? (p.grid <= lim.cu_count ? 1 : 0) : 1;
+                              ? (p.grid <= lim.cu_count && !(c.nbw >= 4 && p.K <= 4096) ? 1 : 0) : 1;
 #define W4A16_RING(XR)                                                                                   \
         hipLaunchKernelGGL((decode_ring_kernel<c.nbw, c.waves, c.d, XR>), dim3(p.grid), dim3(c.waves * 64), \
                            0, st, Wp, x, s, p.M, p.N, p.K, gshift, p.splits, p.slab_chunks, remap, p.grid, y, ws, cnt)
