@@ -690,7 +690,10 @@ def main(argv=None) -> int:
     if a.workload == "prefill" or not a.no_prefill:
         pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
                             a.warmup if a.workload == "prefill" else a.prefill_warmup)
-    mod = bench_moderate(torch, gemm, 30, 3) if (dec is not None and not a.no_prefill) else None
+    # configs[2] is timed with the run's own steps and warm-up (200 and 20 by default, ~90 ms):
+    # after the HBM-bound legs its time per call falls over the first few hundred calls (30 timed
+    # steps after 3 warm-up steps read 29.0 us, after 20 26.5 us, 200 after 20 25.0 us; one box).
+    mod = bench_moderate(torch, gemm, a.steps, a.warmup) if (dec is not None and not a.no_prefill) else None
     c1 = bench_c1(torch, gemm, 40, 3) if (dec is not None and not a.no_c1) else None
     gv = bench_gemv(torch, 20, 3) if (dec is not None and not a.no_prefill) else None
     eager = bench_eager(torch, gemm) if (dec is not None and not a.no_c1) else None
