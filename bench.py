@@ -56,6 +56,7 @@ DECODE_CASES = [("gate_up", 14336, 4096, m) for m in (1, 4, 8, 16)] + \
 PREFILL_CASE = ("mlp70b", 28672, 8192, 2048)
 MODERATE_CASE = ("gate_up", 14336, 4096, 128, 64)          # M=128, G=64
 GRAPH_STEPS = 400                                            # longest timed region captured as one graph
+SIDE_STEPS, SIDE_WARMUP = 200, 20                            # timed and warm-up steps of the side legs
 GEMV_CASES = [("c1_shape", 4096, 4096), ("gate_up", 14336, 4096)]    # (name, N, K) of w4a16_ext.w4a16_gemv
 C1_CASE = ("c1", 4096, 4096, 1)                              # M=1, K=N=4096, G=128
 G = 128
@@ -690,12 +691,13 @@ def main(argv=None) -> int:
     if a.workload == "prefill" or not a.no_prefill:
         pre = bench_prefill(torch, gemm, a.prefill_steps if a.workload == "decode" else a.steps,
                             a.warmup if a.workload == "prefill" else a.prefill_warmup)
-    # configs[2] is timed with the run's own steps and warm-up (200 and 20 by default, ~90 ms):
-    # after the HBM-bound legs its time per call falls over the first few hundred calls (30 timed
-    # steps after 3 warm-up steps read 29.0 us, after 20 26.5 us, 200 after 20 25.0 us; one box).
-    mod = bench_moderate(torch, gemm, a.steps, a.warmup) if (dec is not None and not a.no_prefill) else None
-    c1 = bench_c1(torch, gemm, 40, 3) if (dec is not None and not a.no_c1) else None
-    gv = bench_gemv(torch, 20, 3) if (dec is not None and not a.no_prefill) else None
+    # The side legs (configs[2], configs[0], the baseline GEMV) take SIDE_STEPS after SIDE_WARMUP
+    # whatever --steps is (like the prefill leg's own counts): after the HBM-bound legs the time per
+    # call of configs[2] falls over the first few hundred calls (30 timed steps after 3 warm-up
+    # steps read 29.0 us, 20 after 5 26.5 us, 200 after 20 25.0 us; one box).  ~150 ms in all.
+    mod = bench_moderate(torch, gemm, SIDE_STEPS, SIDE_WARMUP) if (dec is not None and not a.no_prefill) else None
+    c1 = bench_c1(torch, gemm, SIDE_STEPS, SIDE_WARMUP) if (dec is not None and not a.no_c1) else None
+    gv = bench_gemv(torch, SIDE_STEPS, SIDE_WARMUP) if (dec is not None and not a.no_prefill) else None
     eager = bench_eager(torch, gemm) if (dec is not None and not a.no_c1) else None
 
     out = {"metric": "decode GB/s & %HBM peak (M=1..16); prefill TFLOP/s & %MFMA peak (M=2048)"}
