@@ -583,3 +583,32 @@ def test_auto_plan_at_k_beyond_the_256_row_wide_tiles(lib):
     rc, p, err = plan(lib, M=2048, N=4096, K=2**24 + 128, G=128)
     assert rc == 0 and _check(lib, p) == 0
     assert p.kernel not in WIDE_BM or _wide_offsets_fit(WIDE_BM[p.kernel], 2**24 + 128)
+
+
+def test_random_problems_plan_and_pass_the_launch_check(lib):
+    """Seeded random problems (any M up to 8192, N and K on their 16 / 64 grids, both group sizes)
+    on the MI355X and on its compute partitions (SPX 256 CUs, DPX 128, QPX 64, CPX 32): every
+    valid problem gets a plan that the launch-side check accepts, with consistent scratch fields."""
+    import numpy as np
+    rng = np.random.default_rng(20261202)
+    max_slots = lib.w4a16_max_counter_slots()
+    n = 0
+    for _ in range(2500):
+        G = int(rng.choice([64, 128]))
+        K = G * int(rng.integers(1, 300))
+        N = 16 * int(rng.integers(1, 2400))
+        M = int(np.exp(rng.uniform(0, np.log(8192))))
+        cus = int(rng.choice([256, 128, 64, 32]))
+        rc, p, err = plan(lib, M=M, N=N, K=K, G=G, limits=Limits(cus, 160 * 1024, 1024, 950))
+        assert rc == 0, (M, N, K, G, cus, err)
+        assert _check(lib, p) == 0, (M, N, K, G, cus, p.kernel, p.decode_variant, p.splits)
+        assert p.grid >= 1 and p.splits >= 1 and 0 <= p.counter_slots <= max_slots, (M, N, K, G, cus)
+        assert (p.M, p.N, p.K, p.G) == (M, N, K, G)
+        if p.kernel == 0:
+            assert 0 <= p.decode_variant < 32
+        else:
+            assert 1 <= p.kernel <= 24
+        if p.splits == 1 and p.kernel == 0:
+            assert p.workspace_bytes == 0 and p.counter_slots == 0, (M, N, K, G, cus, p.decode_variant)
+        n += 1
+    assert n == 2500

@@ -1,7 +1,8 @@
 """Seeded random-shape sweeps on the GPU, beside the fixed parametrisations of the other files.
 
 * w4a16_gemm: random (M, N, K, G) within the shape contract (N % 16 == 0, K % 64 == 0,
-  K % G == 0), auto routing.  Each result is checked against the oracle within the reference
+  K % G == 0), auto routing; a second sampler puts half of its small-M shapes on the decode
+  route and every sixth shape at a long K.  Each result is checked against the oracle within the reference
   tolerance (max |y - ref| / max |ref| < 2e-3, tests/test_w4a16.py:41-44); shapes that route to
   prefill must also be bitwise equal to forced variant 4, since every prefill config accumulates
   the same k-slot groups in the same order.
@@ -41,6 +42,41 @@ def test_random_shapes_vs_oracle(M, N, K, G):
         torch = torch_cuda()
         assert torch.equal(y, gemm(Wp, x, scales, variant=4)), "prefill configs must be bit-identical"
 
+
+
+def _gemm_shapes_decode_and_long_k(n=32, seed=20261203):
+    """A second sampler: M log-uniform in 1..700; half of the M <= 16 shapes rounded onto the
+    decode route's grid (N % 64 == 0, K % 512 == 0, kernel.cu:242-249), which the sampler above
+    rarely meets; every sixth shape a long K (8256..16384: the canonical segmented order)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        G = int(rng.choice([64, 128]))
+        M = int(np.exp(rng.uniform(0.0, np.log(700.0))))
+        if i % 6 == 5:
+            K = G * int(rng.integers(8256 // G + 1, 16384 // G + 1))
+            N = 16 * int(rng.integers(1, 65))
+        else:
+            K = G * int(rng.integers(1, 41))
+            N = 16 * int(rng.integers(1, 201))
+        if M <= 16 and i % 2 == 0:
+            N, K = -(-N // 64) * 64, max(1, K // 512) * 512
+        out.append((M, N, K, G))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,G", _gemm_shapes_decode_and_long_k())
+def test_random_decode_and_long_k_shapes_vs_oracle(M, N, K, G):
+    torch = torch_cuda()
+    import w4a16_opt
+    info = w4a16_opt.plan_info(M, N, K, G)
+    print(f"random gemm M={M} N={N} K={K} G={G}: {info['kernel_name']} splits {info['splits']}", flush=True)
+    x, q, scales, Wp, key = make_problem(M, N, K, G, seed=M)
+    y = gemm(Wp, x, scales)
+    assert_close(y, ref_gemm(x, q, scales, G, key))
+    if not (M <= 16 and N % 64 == 0 and K % 512 == 0):
+        assert torch.equal(y, gemm(Wp, x, scales, variant=4)), "prefill configs must be bit-identical"
 
 def _gemv_shapes(n=24, seed=77):
     rng = np.random.default_rng(seed)
