@@ -360,7 +360,8 @@ def test_gcn_arch_name_parse(lib, name, want):
     (1, 10240, 8192, (29, 1)), (4, 10240, 8192, (19, 1)), (8, 10240, 8192, (31, 1)),  # 70B qkv: K = 8192, 640 blocks
     (16, 10240, 8192, (16, 1)), (4, 8192, 8192, (26, 1)), (16, 8192, 8192, (20, 1)),  # 70B o: two-block tiles fit
     (16, 28672, 4096, (12, 1)),                                              # ring tiles would need two rounds
-    (16, 4096, 4096, (19, 1)), (16, 6144, 4096, (20, 1)),                    # qkv: 384 single-block rings = 2 rounds
+    (1, 4096, 4096, (19, 1)), (16, 4096, 4096, (19, 1)),                     # configs[0]: two pairs in flight
+    (16, 6144, 4096, (20, 1)),                                               # qkv: 384 single-block rings = 2 rounds
     (1, 6144, 4096, (29, 1)), (4, 6144, 4096, (26, 1)), (8, 6144, 4096, (26, 1)),  # qkv: two-block rings below 16 rows
     (1, 8192, 28672, (26, 1)), (4, 8192, 28672, (30, 1)), (8, 8192, 28672, (26, 1)),  # 70B down: 512 single blocks
     (16, 8192, 28672, (16, 2)),

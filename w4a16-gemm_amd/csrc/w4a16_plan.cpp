@@ -334,7 +334,10 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             //    traffic per block grows, two-block tiles of 4 waves split in two (M = 16: 11.95
             //    vs 12.57 us for 8 waves, in two sweeps);
             //  * short K, moderate N (K = N = 4096): single-block rings of 8 waves, else two-block
-            //    rings of 4;
+            //    rings of 4; at one token row with two pairs in flight up to K = 4096 where the
+            //    single-block tiles fit one per CU (configs[0]: 4.03-4.04 vs 4.09-4.10 us for three
+            //    pairs, G = 128 and 64, order-rotated on two boxes) and three above (qkv, N = 6144:
+            //    5.33 vs 5.57 us);
             //  * more single-block tiles than CUs (qkv N = 6144, Llama-3-70B down N = 8192): two-block
             //    rings of 8 waves from 2 token rows up, which give every CU one tile (70B down
             //    M = 8: 28.5 vs 33.2 us for the single-block rings; qkv M = 8: 6.08 vs 6.46 us);
@@ -363,6 +366,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             Cand longk_small_m[] = {{19, 1}, {22, 2}, {22, 2}};
             Cand longk_large_m[] = {{20, 2}, {22, 2}, {19, 1}};
             Cand shortk_m1[] = {{29, 1}, {19, 1}, {14, 1}};
+            Cand shortk_m1_fit[] = {{19, 1}, {29, 1}, {14, 1}};
             Cand shortk[] = {{19, 1}, {20, 1}, {21, 1}};
             Cand many_m1[] = {{26, 1}, {29, 1}, {19, 1}};
             Cand many_longk_m4[] = {{30, 1}, {26, 1}, {29, 1}};
@@ -394,7 +398,8 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             else if (KC >= 128 && many_blocks)
                 list = M <= 1 ? many_m1 : M <= 4 ? many_longk_m4 : M <= 8 ? many_small_m : many_longk_large_m;
             else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
-            else list = M <= 1 ? shortk_m1 : M <= 8 && many_blocks ? many_small_m : shortk;
+            else list = M <= 1 ? (!many_blocks && KC <= 64 ? shortk_m1_fit : shortk_m1)
+                               : M <= 8 && many_blocks ? many_small_m : shortk;
             for (int i = 0; i < n && var < 0; ++i)
                 if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus &&
                     (M <= 8 || one_round(list[i].v, list[i].sp))) {
