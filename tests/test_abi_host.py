@@ -362,7 +362,8 @@ def test_gcn_arch_name_parse(lib, name, want):
     (16, 28672, 4096, (12, 1)),                                              # ring tiles would need two rounds
     (1, 4096, 4096, (19, 1)), (16, 4096, 4096, (19, 1)),                     # configs[0]: two pairs in flight
     (16, 6144, 4096, (20, 1)),                                               # qkv: 384 single-block rings = 2 rounds
-    (1, 6144, 4096, (29, 1)), (4, 6144, 4096, (26, 1)), (8, 6144, 4096, (26, 1)),  # qkv: two-block rings below 16 rows
+    (1, 6144, 4096, (29, 1)), (4, 6144, 4096, (26, 1)), (6, 6144, 4096, (22, 1)),  # qkv: two-block rings below 16 rows,
+    (8, 6144, 4096, (22, 1)),                                                # one pair in flight from 5 rows
     (1, 8192, 28672, (26, 1)), (4, 8192, 28672, (30, 1)), (8, 8192, 28672, (26, 1)),  # 70B down: 512 single blocks
     (16, 8192, 28672, (16, 2)),
     (1, 3584, 18944, (21, 1)), (16, 3584, 18944, (21, 1)),                  # odd chunks per 8-wave ring: generic rings

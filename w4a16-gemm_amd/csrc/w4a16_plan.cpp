@@ -340,7 +340,9 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             //    5.33 vs 5.57 us);
             //  * more single-block tiles than CUs (qkv N = 6144, Llama-3-70B down N = 8192): two-block
             //    rings of 8 waves from 2 token rows up, which give every CU one tile (70B down
-            //    M = 8: 28.5 vs 33.2 us for the single-block rings; qkv M = 8: 6.08 vs 6.46 us);
+            //    M = 8: 28.5 vs 33.2 us for the single-block rings; qkv M = 8: 6.08 vs 6.46 us), on
+            //    short K with one pair in flight from 5 rows (qkv M = 8: 5.48 vs 5.85 us, M = 6: 5.37
+            //    vs 5.67, order-rotated; M = 4 level);
             //    16 waves at M <= 4 on long K (70B down M = 4: 26.3 vs 27.7 us), 4-block rings of 4
             //    waves split in two above 8 rows (70B down M = 16: 30.6 vs 35.6 us).
             // Above 8 token rows a ring's LDS allows one or two workgroups per CU, so a shape is
@@ -371,6 +373,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
             Cand many_m1[] = {{26, 1}, {29, 1}, {19, 1}};
             Cand many_longk_m4[] = {{30, 1}, {26, 1}, {29, 1}};
             Cand many_small_m[] = {{26, 1}, {22, 1}, {19, 1}};
+            Cand many_mid_m[] = {{22, 1}, {26, 1}, {19, 1}};
             Cand many_longk_large_m[] = {{16, 2}, {26, 1}, {20, 2}};
             // K = 8192 with many blocks (Llama-3-70B o, qkv): shorter streams than the 70B down
             // projection the lists above come from, so no split; two-block tiles while they fit one
@@ -399,7 +402,7 @@ extern "C" int w4a16_plan_create(const w4a16_problem* prob, int variant, const w
                 list = M <= 1 ? many_m1 : M <= 4 ? many_longk_m4 : M <= 8 ? many_small_m : many_longk_large_m;
             else if (KC >= 128) list = M <= 4 ? longk_m4 : M <= 8 ? longk_small_m : longk_large_m;
             else list = M <= 1 ? (!many_blocks && KC <= 64 ? shortk_m1_fit : shortk_m1)
-                               : M <= 8 && many_blocks ? many_small_m : shortk;
+                               : M <= 8 && many_blocks ? (M <= 4 ? many_small_m : many_mid_m) : shortk;
             for (int i = 0; i < n && var < 0; ++i)
                 if (ok(list[i].v, list[i].sp) && (int64_t)ntiles_of(list[i].v) * list[i].sp * 2 >= cus &&
                     (M <= 8 || one_round(list[i].v, list[i].sp))) {
